@@ -1,0 +1,215 @@
+"""Benchmark of the paged-KV decode hot path on one MI355X.
+
+A step is one layer's decode-time work on the paged cache, in the reference's
+order (models/qwen3.rs:199-208): KV append of one new token per sequence
+(reshape_and_cache), then paged decode attention over every sequence's context.
+Default workload: BASELINE config 3 (Qwen3-8B shape, 32 q / 8 kv heads, D 128,
+bf16, block 256, batch 64, context U[2048, 8192], 8192-block pool), synthetic
+N(0,1) data resident in HBM, steps rotating over distinct layers of the
+[2, layers, NB, 256, 8, 128] buffer so that no step re-reads what the previous
+one left in the 256 MB MALL.
+
+Prints ONE JSON line.  value = algorithmic bytes of (append + attention) per
+step / wall time per step.  The dominant kernel pair (split-KV attention +
+merge) is also timed with HIP events on the stream it runs on -> roofline.
+cpu_baseline = the C oracle (test infrastructure, reference semantics) on a
+bounded sample of the same workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+sys.path.insert(0, str(REPO / "vllm-oxide_amd"))
+sys.path.insert(0, str(REPO))
+
+HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+
+
+def cpu_baseline(cfg, seed: int, threads: int, min_seconds: float = 10.0) -> dict:
+    """Oracle append + attention on the first `n` sequences of the workload."""
+    import numpy as np
+
+    import oracle
+    from oxide_paged_kv.workload import make_decode_step
+
+    n = 8
+    st = make_decode_step(cfg, seed=seed, batch=n)
+    rng = np.random.default_rng(seed)
+    rows = st.block_rows
+    used = np.concatenate(rows)
+    nb = len(used)
+    remap = {int(b): i for i, b in enumerate(used)}
+    table = np.zeros_like(st.block_table)
+    for b, r in enumerate(rows):
+        table[b, :len(r)] = [remap[int(x)] for x in r]
+    shape = (nb, cfg.block_size, cfg.num_kv_heads, cfg.head_dim)
+
+    def bits(shape):
+        return oracle.f32_to_bf16_bits(rng.standard_normal(size=shape, dtype=np.float32)).reshape(shape)
+
+    kc, vc = bits(shape), bits(shape)
+    q = bits((n, cfg.num_heads, cfg.head_dim))
+    knew = bits((n, cfg.num_kv_heads, cfg.head_dim))
+    vnew = bits((n, cfg.num_kv_heads, cfg.head_dim))
+    slots = np.array([table[b, (L - 1) // cfg.block_size] * cfg.block_size + (L - 1) % cfg.block_size
+                      for b, L in enumerate(st.context_lens.astype(np.int64))], dtype=np.int64)
+    scale = 1 / math.sqrt(cfg.head_dim)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.reshape_and_cache(knew, vnew, kc, vc, slots)
+        oracle.paged_decode_attention(q, kc, vc, st.cu_seqlens_k, table, scale, cfg.window_left,
+                                      "bf16", threads=threads)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            break
+    step_bytes = st.attn_bytes() + st.append_bytes()
+    return {"value": round(step_bytes * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{n} sequences of the same workload (seed {seed}, {int(st.context_lens.sum())} keys), "
+                      f"append + fp32-accumulated attention, {reps} reps in {dt:.1f} s"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=0, help="distinct layers to rotate over (0 = auto)")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--stream-copy", action="store_true", default=True)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        return 2
+
+    import numpy as np
+    import torch
+
+    import oxide_paged_kv as ox
+    from oxide_paged_kv.workload import CONFIGS, make_decode_step
+
+    cfg = CONFIGS[args.config]
+    dev = torch.device("cuda:0")
+    st = make_decode_step(cfg, seed=args.seed)
+    layers = args.layers or (cfg.layers if cfg.layers > 1 else 4)
+    NB, BS, H, D = st.pool_blocks, cfg.block_size, cfg.num_kv_heads, cfg.head_dim
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    # PagedKVCache buffer [2, L, NB, BS, H, D] (attention/mod.rs:55-85).
+    buf = torch.empty((2, layers, NB, BS, H, D), dtype=torch.bfloat16, device=dev)
+    for kv in range(2):
+        for layer in range(layers):
+            buf[kv, layer].normal_(generator=g)
+    q = torch.randn((layers, cfg.batch, cfg.num_heads, D), generator=g, device=dev).bfloat16()
+    knew = torch.randn((layers, cfg.batch, H, D), generator=g, device=dev).bfloat16()
+    vnew = torch.randn((layers, cfg.batch, H, D), generator=g, device=dev).bfloat16()
+    # Metadata uploaded once per step for all layers (not once per layer).
+    sm = torch.from_numpy(st.slot_mapping).to(dev)
+    cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(dev)
+    bt = torch.from_numpy(st.block_table).to(dev)
+    out = torch.empty((cfg.batch, cfg.num_heads, D), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(ox.workspace_size(cfg.batch, cfg.num_heads, H, D, st.max_seqlen_k), 1),
+                     dtype=torch.uint8, device=dev)
+    scale = 1 / math.sqrt(D)
+    window = None if cfg.window_left < 0 else cfg.window_left
+
+    def step(i, ev=None):
+        layer = i % layers
+        kc, vc = buf[0, layer], buf[1, layer]
+        if ev:
+            ev[0].record()
+        ox.reshape_and_cache(knew[layer], vnew[layer], kc, vc, sm)
+        if ev:
+            ev[1].record()
+        ox.decode_attn(q[layer], kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out, workspace=ws)
+        if ev:
+            ev[2].record()
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(args.warmup + i, evs[i])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    app_ms = [e[0].elapsed_time(e[1]) for e in evs]
+    att_ms = [e[1].elapsed_time(e[2]) for e in evs]
+    ms_per_step = wall * 1e3 / args.steps
+    attn_bytes, app_bytes = st.attn_bytes(), st.append_bytes()
+    attn_us = float(np.mean(att_ms)) * 1e3
+    app_us = float(np.mean(app_ms)) * 1e3
+    attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
+    app_gbps = app_bytes / (app_us * 1e-6) / 1e9
+    value = (attn_bytes + app_bytes) / (ms_per_step * 1e-3) / 1e9
+
+    extra = {}
+    if args.stream_copy:
+        # Achievable-bandwidth calibration: copy_blocks over 1 MiB blocks (read+write).
+        nblk = 2048
+        cbuf = torch.empty((2, 2 * nblk, BS, H, D), dtype=torch.bfloat16, device=dev)
+        pairs = torch.stack([torch.arange(nblk), torch.arange(nblk, 2 * nblk)], 1).to(dev)
+        for _ in range(3):
+            ox.copy_blocks(cbuf[0], cbuf[1], pairs)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            ox.copy_blocks(cbuf[0], cbuf[1], pairs)
+        e1.record()
+        torch.cuda.synchronize()
+        cbytes = 2 * nblk * 2 * (BS * H * D * 2)
+        extra["stream_copy_gbps"] = round(cbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9, 1)
+        del cbuf
+
+    res = {
+        "metric": "paged-decode attn KV-read GB/s (% HBM peak) + append GB/s, Qwen3-8B shape",
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) K/V/Q, seeded random block tables",
+        "config": {"workload": cfg.name, "batch": cfg.batch, "num_heads": cfg.num_heads,
+                   "num_kv_heads": H, "head_dim": D, "block_size": BS, "pool_blocks": NB,
+                   "ctx": [cfg.ctx_lo, cfg.ctx_hi], "window_left": cfg.window_left,
+                   "layers_rotated": layers, "split_tokens": ox.split_tokens(cfg.batch, H, st.max_seqlen_k),
+                   "total_keys": int(st.context_lens.sum())},
+        "attn_us": round(attn_us, 2),
+        "attn_kv_read_gbps": round(st.kv_read_bytes() / (attn_us * 1e-6) / 1e9, 1),
+        "attn_gbps": round(attn_gbps, 1),
+        "attn_hbm_frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
+        "append_us": round(app_us, 2),
+        "append_gbps": round(app_gbps, 1),
+        "tokens_per_s": round(cfg.batch / (ms_per_step * 1e-3), 1),
+        "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "paged_decode_split + paged_decode_merge (one attention call)",
+                     "algorithmic_bytes": attn_bytes},
+        **extra,
+    }
+    if not args.no_cpu_baseline:
+        threads = min(16, os.cpu_count() or 1)
+        res["cpu_baseline"] = cpu_baseline(cfg, args.seed, threads)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,153 @@
+/*
+ * oxide_paged_kv.h — C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and a
+ * hipStream_t passed as `void*`.  Nothing here allocates device memory: the
+ * caller owns every buffer, including the split-KV workspace of the decode
+ * attention.  All launches are asynchronous on the given stream (NULL = the
+ * default stream).  Entry points return void, as the reference's do; argument
+ * and launch errors are recorded per host thread and read back with
+ * oxide_last_error() / oxide_error_string().
+ *
+ * Data layout (shared with the reference, crates/vllm-oxide/src/utils.rs:46-61
+ * and crates/vllm-oxide/src/attention/mod.rs:78-85):
+ *   physical buffer  [2, num_layers, num_blocks, block_size, num_kv_heads, head_dim]
+ *   per-layer view   key_cache / value_cache = [num_blocks, block_size, num_kv_heads, head_dim]
+ *   slot             block_id * block_size + offset_in_block  (row index of that view)
+ *
+ * dtype codes (crates/vllm-oxide/src/attention/kernels.rs:97-104):
+ *   0 = f16, 1 = bf16, 2 = f32.
+ */
+#ifndef OXIDE_PAGED_KV_H
+#define OXIDE_PAGED_KV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  OXIDE_DTYPE_F16 = 0,
+  OXIDE_DTYPE_BF16 = 1,
+  OXIDE_DTYPE_F32 = 2,
+};
+
+enum {
+  OXIDE_OK = 0,
+  OXIDE_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative count, bad stride */
+  OXIDE_ERR_UNSUPPORTED_DTYPE = 2,
+  OXIDE_ERR_UNSUPPORTED_SHAPE = 3, /* head_dim / group size / block size not built */
+  OXIDE_ERR_WORKSPACE_TOO_SMALL = 4,
+  OXIDE_ERR_HIP = 1000 /* OXIDE_ERR_HIP + hipError_t of a failed launch */
+};
+
+/*
+ * KV append.  Replaces `extern "C" void reshape_and_cache(...)` of
+ * crates/vllm-oxide/kernels/reshape_and_cache.cu:30-41 (Rust binding
+ * crates/vllm-oxide/src/attention/kernels.rs:15-26); same symbol, same
+ * parameters, `stream` is a hipStream_t.
+ *
+ * For token t in [0, num_tokens) with slot = slot_mapping[t] >= 0:
+ *   key_cache  [slot * H*D + e] = key  [t * H*D + e]
+ *   value_cache[slot * H*D + e] = value[t * H*D + e]    for e < H*D
+ * where H = num_kv_heads, D = head_dim.  slot == -1 (the reference's sentinel,
+ * kv_cache_manager.rs:128-131) leaves the cache untouched; any other negative
+ * slot is treated the same way.  key/value are contiguous [T, H, D].  The copy
+ * is bitwise, so it is bit-exact for every dtype.
+ */
+void reshape_and_cache(const void* key, const void* value, void* key_cache, void* value_cache,
+                       const int64_t* slot_mapping, int64_t num_tokens, int64_t num_kv_heads,
+                       int64_t head_dim, int dtype, void* stream);
+
+/*
+ * Block copy for prefix-cache copy-on-write.  Replaces `extern "C" void
+ * copy_blocks(...)` of crates/vllm-oxide/kernels/copy_blocks.cu:30-38 (Rust
+ * binding crates/vllm-oxide/src/attention/kernels.rs:28-36); same symbol and
+ * parameters.
+ *
+ * block_mapping is a device int64 array [num_pairs, 2] of (src, dst) block
+ * ids; block_stride is in ELEMENTS (block_size * num_kv_heads * head_dim,
+ * kernels.rs:164-165).  For each pair, block dst of key_cache and of
+ * value_cache becomes a bitwise copy of block src.  Precondition (as in the
+ * reference, where it is unchecked): no dst block is also the src of another
+ * pair in the same call.
+ */
+void copy_blocks(void* key_cache, void* value_cache, const int64_t* block_mapping,
+                 int64_t num_pairs, int64_t block_stride, int dtype, void* stream);
+
+/*
+ * Prefix-hit block gather.  No reference counterpart (the reference never
+ * reads prefix-hit blocks back from the paged cache,
+ * crates/vllm-oxide/src/engine/mod.rs:172,195); it follows copy_blocks'
+ * conventions.  For i < num_blocks:
+ *   key_dst  [i * block_stride + e] = key_cache  [block_ids[i] * block_stride + e]
+ *   value_dst[i * block_stride + e] = value_cache[block_ids[i] * block_stride + e]
+ * so key_dst/value_dst come out as contiguous [num_blocks * block_size, H, D].
+ * value_dst / value_cache may both be NULL to gather keys only.
+ */
+void gather_blocks(void* key_dst, void* value_dst, const void* key_cache, const void* value_cache,
+                   const int32_t* block_ids, int64_t num_blocks, int64_t block_stride, int dtype,
+                   void* stream);
+
+/*
+ * Paged decode attention with GQA, optional left sliding window and split-KV
+ * (flash-decoding).  Replaces the decode call of
+ * candle_flash_attn::flash_attn_varlen_paged_windowed made at
+ * crates/vllm-oxide/src/attention/flash_attn.rs:52-67 (argument meanings in
+ * research/prototype-candle-stack/src/main.rs:219-234).
+ *
+ *   out          [batch, num_heads, head_dim]        written (caller-allocated)
+ *   q            [batch, num_heads, head_dim]        one query token per sequence
+ *   k_cache      [num_blocks, page_block_size, num_kv_heads, head_dim]
+ *   v_cache      same
+ *   cu_seqlens_k uint32 [batch + 1], prefix sums of context lengths
+ *                (build_decode_metadata, attention/metadata.rs:20-47)
+ *   block_table  int32 [batch, max_blocks_per_seq], rows padded with 0
+ *                (flash_attn.rs:74-86); only the first ceil(L_b / page_block_size)
+ *                entries of row b are read
+ *   num_blocks   blocks in k_cache / v_cache (dim 0 of the FA tensors); block
+ *                ids outside [0, num_blocks) are clamped into range, so a bad
+ *                table gives a wrong answer but never an out-of-bounds access
+ *   max_seqlen_k max over b of L_b; sizes the split grid and the workspace.
+ *                Lengths above it are clamped to it.
+ *   window_left  -1 = unbounded (the reference passes None); w >= 0 attends to
+ *                keys [max(0, L_b - 1 - w), L_b - 1]
+ *   softmax_scale scale applied to q.k before the softmax (1/sqrt(head_dim) in
+ *                the reference, models/qwen3.rs:204)
+ *
+ * Query head h reads kv head h / (num_heads / num_kv_heads).  A sequence with
+ * L_b == 0 produces zeros.  Supported: dtype f16 or bf16, head_dim 64 or 128,
+ * num_heads / num_kv_heads in {1, 2, 4, 8, 16}, page_block_size a positive
+ * multiple of 16.  workspace must hold
+ * paged_decode_attention_workspace_size(...) bytes for the same arguments.
+ */
+void paged_decode_attention(void* out, const void* q, const void* k_cache, const void* v_cache,
+                            const uint32_t* cu_seqlens_k, const int32_t* block_table,
+                            int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
+                            int64_t num_heads,
+                            int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
+                            int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
+                            void* workspace, size_t workspace_bytes, int dtype, void* stream);
+
+/* Bytes of workspace paged_decode_attention needs for these arguments. */
+size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
+                                             int64_t num_kv_heads, int64_t head_dim,
+                                             int64_t max_seqlen_k);
+
+/* Tokens per KV split chosen for these arguments (a multiple of 256). */
+int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
+                                            int64_t max_seqlen_k);
+
+/* Error state of the calling host thread: the first error since the last
+ * oxide_clear_error(), or OXIDE_OK. */
+int oxide_last_error(void);
+void oxide_clear_error(void);
+const char* oxide_error_string(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OXIDE_PAGED_KV_H */

@@ -1,0 +1,82 @@
+/*
+ * CPU oracle for the paged-KV hot path.  TEST INFRASTRUCTURE ONLY: it is the
+ * checker that tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg
+ * compare the HIP library against.  The product library never links or calls
+ * it, and nothing in the product falls back to it.
+ *
+ * Each function restates the reference algorithm it names (file:line under the
+ * vllm-oxide tree) as plain loops.  How each one is pinned (golden vectors,
+ * closed forms, independent brute force) is written next to it.
+ */
+#ifndef OXIDE_ORACLE_H
+#define OXIDE_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* 16-bit float formats <-> fp32.  dtype: 0 = f16, 1 = bf16 (kernels.rs:97-104). */
+float oracle_half_to_float(uint16_t h, int dtype);
+uint16_t oracle_float_to_half(float f, int dtype); /* round to nearest even */
+
+/* KvCacheManager::compute_slot_mapping, engine/kv_cache_manager.rs:115-135. */
+void oracle_compute_slot_mapping(const int64_t* block_table, int64_t table_len,
+                                 int64_t block_size, int64_t token_offset, int64_t num_tokens,
+                                 int64_t* slot_mapping);
+
+/* build_decode_metadata, attention/metadata.rs:20-47 (cu_seqlens_q/k have
+ * batch + 1 entries; returns max_seqlen_k). */
+int64_t oracle_build_decode_metadata(const uint32_t* context_lens, int64_t batch,
+                                     uint32_t* cu_seqlens_q, uint32_t* cu_seqlens_k);
+
+/* block_table_tensor, attention/flash_attn.rs:74-86: ragged rows (concatenated
+ * in `flat`, row b has row_lens[b] entries) padded with 0 to [batch, max_len].
+ * Returns max_len; `out` must hold batch * max_len entries. */
+int64_t oracle_pad_block_table(const int32_t* flat, const int64_t* row_lens, int64_t batch,
+                               int32_t* out);
+
+/* reshape_and_cache kernel, kernels/reshape_and_cache.cu:6-28 (bitwise row
+ * copy of esize-byte elements; slot == -1 skipped). */
+void oracle_reshape_and_cache(const void* key, const void* value, void* key_cache,
+                              void* value_cache, const int64_t* slot_mapping, int64_t num_tokens,
+                              int64_t num_kv_heads, int64_t head_dim, int esize);
+
+/* copy_blocks kernel, kernels/copy_blocks.cu:8-28 (pairs applied in order). */
+void oracle_copy_blocks(void* key_cache, void* value_cache, const int64_t* block_mapping,
+                        int64_t num_pairs, int64_t block_stride, int esize);
+
+/* Prefix-hit gather (no reference counterpart): dst block i = cache block ids[i]. */
+void oracle_gather_blocks(void* key_dst, void* value_dst, const void* key_cache,
+                          const void* value_cache, const int32_t* block_ids, int64_t num_blocks,
+                          int64_t block_stride, int esize);
+
+/* Paged decode attention (the decode call of flash_attn_varlen_paged_windowed,
+ * attention/flash_attn.rs:52-67): for each sequence b and query head h, keys
+ * j in [lo, L_b), L_b = cu_seqlens_k[b+1] - cu_seqlens_k[b],
+ * lo = window_left < 0 ? 0 : max(0, L_b - 1 - window_left), key j at cache row
+ * block_table[b * max_blocks + j / block_size] * block_size + j % block_size,
+ * kv head h / (num_heads / num_kv_heads);
+ *   out[b,h,:] = sum_j softmax_j(scale * q.K_j) V_j.
+ * Inputs are 16-bit (dtype 0/1).  Arithmetic in fp32 (use_f64 = 0: dot
+ * products and sums accumulated in index order, two-pass softmax with expf) or
+ * fp64 (use_f64 = 1).  Writes fp32 `out` [batch, num_heads, head_dim]; an
+ * empty sequence gives zeros.  Parallel over (b, kv head) on `threads` OpenMP
+ * threads (<= 0: OpenMP default). */
+void oracle_paged_decode_attention(float* out, const uint16_t* q, const uint16_t* k_cache,
+                                   const uint16_t* v_cache, const uint32_t* cu_seqlens_k,
+                                   const int32_t* block_table, int64_t max_blocks, int64_t batch,
+                                   int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                   int64_t block_size, int32_t window_left, float softmax_scale,
+                                   int dtype, int use_f64, int threads);
+
+/* XXH64 (public xxHash spec, 64-bit variant) of `len` bytes with `seed`. */
+uint64_t oracle_xxh64(const void* data, size_t len, uint64_t seed);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OXIDE_ORACLE_H */

@@ -1,0 +1,173 @@
+"""GPU parity of paged decode attention (split-KV, GQA, window) against the oracle.
+
+Tolerance (the target's, for bf16/f16 output vs an fp32-accumulated reference):
+max-abs 2e-2 and max-rel 1e-2, checked by helpers.assert_attn_close.  The oracle
+(oracle/oxide_oracle.c, fp32 accumulate) is itself pinned against numpy fp64 in
+tests/test_oracle.py.
+"""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import assert_attn_close, normal_bits, to_bits, to_f32, to_torch
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(device, q, kc, vc, cu, table, max_seqlen, scale, window, dtype):
+    import torch
+    import oxide_paged_kv as ox
+
+    out = ox.decode_attn(to_torch(q, dtype, device), to_torch(kc, dtype, device),
+                         to_torch(vc, dtype, device),
+                         torch.from_numpy(cu.view(np.int32)).to(device),
+                         torch.from_numpy(np.ascontiguousarray(table, dtype=np.int32)).to(device),
+                         max_seqlen, scale, None if window < 0 else window, kc.shape[1])
+    torch.cuda.synchronize()
+    return out
+
+
+def _case(seed, B, Hq, Hkv, D, BS, NB, lens, dtype="bf16"):
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens, dtype=np.int64)
+    nblk = (lens + BS - 1) // BS
+    assert nblk.sum() <= NB
+    perm = rng.permutation(NB).astype(np.int32)
+    width = max(int(nblk.max()), 1)
+    table = np.zeros((B, width), np.int32)
+    pos = 0
+    for b in range(B):
+        table[b, :nblk[b]] = perm[pos:pos + nblk[b]]
+        pos += nblk[b]
+    cu = np.zeros(B + 1, np.uint32)
+    cu[1:] = np.cumsum(lens)
+    q = normal_bits(rng, (B, Hq, D), dtype)
+    kc = normal_bits(rng, (NB, BS, Hkv, D), dtype)
+    vc = normal_bits(rng, (NB, BS, Hkv, D), dtype)
+    return q, kc, vc, cu, table, int(lens.max())
+
+
+CASES = [
+    # (B, Hq, Hkv, D, BS, NB, lens, window, dtype)
+    (4, 16, 8, 128, 256, 64, [300, 1000, 557, 999], -1, "bf16"),        # cfg1 shape
+    (3, 32, 8, 128, 256, 40, [2048, 4097, 3000], -1, "bf16"),           # G=4 (Qwen3-8B)
+    (2, 64, 8, 128, 256, 80, [9000, 513], -1, "bf16"),                  # G=8 (Qwen3-32B)
+    (3, 8, 8, 128, 256, 20, [1, 255, 256], -1, "bf16"),                 # G=1, page edges
+    (2, 4, 2, 64, 256, 20, [700, 33], -1, "f16"),                       # G=2, D=64, f16
+    (2, 32, 2, 64, 32, 120, [1500, 77], -1, "bf16"),                    # G=16, BS=32
+    (3, 16, 8, 128, 16, 400, [1000, 17, 16], -1, "f16"),                # BS=16
+    (4, 32, 8, 128, 256, 64, [5000, 4097, 100, 4096], 4096, "bf16"),    # window 4096
+    (3, 16, 8, 128, 256, 30, [2000, 700, 101], 100, "bf16"),            # window 100
+    (2, 16, 8, 128, 256, 10, [600, 5], 0, "bf16"),                      # window 0: last key only
+    (5, 16, 8, 128, 256, 20, [0, 10, 0, 1, 300], -1, "bf16"),           # empty sequences
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
+def test_decode_vs_oracle(device, case):
+    B, Hq, Hkv, D, BS, NB, lens, window, dtype = case
+    q, kc, vc, cu, table, mx = _case(11, B, Hq, Hkv, D, BS, NB, lens, dtype)
+    scale = 1.0 / math.sqrt(D)
+    print(f"decode case B={B} Hq={Hq} Hkv={Hkv} D={D} BS={BS} lens={lens} window={window} {dtype}", flush=True)
+    got = to_f32(_run(device, q, kc, vc, cu, table, mx, scale, window, dtype))
+    want = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype)
+    assert_attn_close(got, want)
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert not got[b].any()
+
+
+def test_decode_reference_smoke_shape(device):
+    """attention/mod.rs:277-323 flash_attn_decode_runs: ctx 32, 4 heads, 4 kv heads,
+    D 64, one block of 256 -> shape [1, 4, 64], no NaN (and here also parity)."""
+    q, kc, vc, cu, table, mx = _case(12, 1, 4, 4, 64, 256, 1, [32])
+    out = _run(device, q, kc, vc, cu, table, mx, 1 / 8.0, -1, "bf16")
+    assert tuple(out.shape) == (1, 4, 64)
+    got = to_f32(out)
+    assert not np.isnan(got).any()
+    assert_attn_close(got, oracle.paged_decode_attention(q, kc, vc, cu, table, 1 / 8.0))
+
+
+def test_decode_constant_v_closed_form(device):
+    """V rows all equal -> every output row is that V row (any q, any window)."""
+    q, kc, vc, cu, table, mx = _case(13, 3, 32, 8, 128, 256, 40, [3000, 257, 1])
+    row = normal_bits(np.random.default_rng(0), (8, 128))
+    vc[:] = row[None, None]
+    out = to_f32(_run(device, q, kc, vc, cu, table, mx, 0.0883883, -1, "bf16"))
+    want = np.repeat(oracle.bf16_bits_to_f32(row), 4, axis=0)
+    for b in range(3):
+        np.testing.assert_allclose(out[b], want, atol=1e-2, rtol=1e-2)
+
+
+def test_decode_placement_invariance_bit_exact(device):
+    """Moving the pages to other physical blocks (and re-pointing the table) must
+    not change one output bit: the reduction order depends on logical positions only."""
+    q, kc, vc, cu, table, mx = _case(14, 4, 32, 8, 128, 256, 64, [5000, 4097, 100, 4096])
+    a = to_bits(_run(device, q, kc, vc, cu, table, mx, 0.0883883, -1, "bf16"))
+    perm = np.random.default_rng(1).permutation(64)
+    inv = np.argsort(perm)
+    kc2, vc2 = kc[inv], vc[inv]  # block i moves to slot perm[i]
+    table2 = perm[table].astype(np.int32)
+    b = to_bits(_run(device, q, kc2, vc2, cu, table2, mx, 0.0883883, -1, "bf16"))
+    assert np.array_equal(a, b)
+
+
+def test_decode_window_at_least_len_equals_no_window(device):
+    q, kc, vc, cu, table, mx = _case(15, 3, 16, 8, 128, 256, 30, [2000, 700, 101])
+    a = to_bits(_run(device, q, kc, vc, cu, table, mx, 0.0883883, -1, "bf16"))
+    b = to_bits(_run(device, q, kc, vc, cu, table, mx, 0.0883883, 5000, "bf16"))
+    assert np.array_equal(a, b)
+
+
+def test_decode_ignores_padding_and_stale_nan(device):
+    """Slots past L in the last page and padded table entries (block 0) hold NaN;
+    the output must not see them."""
+    q, kc, vc, cu, table, mx = _case(16, 2, 16, 8, 128, 256, 12, [300, 20])
+    nan = np.uint16(0x7FC0)
+    used = set()
+    for b, L in enumerate([300, 20]):
+        nb = (L + 255) // 256
+        used.update(table[b, :nb].tolist())
+        last = table[b, nb - 1]
+        kc[last, L % 256 or 256:] = nan
+        vc[last, L % 256 or 256:] = nan
+    for blk in range(12):
+        if blk not in used:
+            kc[blk] = nan
+            vc[blk] = nan
+    got = to_f32(_run(device, q, kc, vc, cu, table, mx, 0.0883883, -1, "bf16"))
+    want = oracle.paged_decode_attention(q, kc, vc, cu, table, 0.0883883)
+    assert_attn_close(got, want)
+
+
+def test_decode_cfg3_full_size_sampled(device):
+    """Full cfg3 (Qwen3-8B, B=64, ctx U[2048,8192], 8192-block pool): the whole batch
+    runs on the GPU; 6 sampled sequences are checked against the oracle."""
+    import torch
+    import oxide_paged_kv as ox
+    from oxide_paged_kv.workload import CONFIGS, make_decode_step
+
+    st = make_decode_step(CONFIGS[3], seed=7)
+    c = st.cfg
+    g = torch.Generator(device=device).manual_seed(7)
+    shape = (st.pool_blocks, c.block_size, c.num_kv_heads, c.head_dim)
+    kc = torch.randn(shape, generator=g, device=device).bfloat16()
+    vc = torch.randn(shape, generator=g, device=device).bfloat16()
+    q = torch.randn((c.batch, c.num_heads, c.head_dim), generator=g, device=device).bfloat16()
+    cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
+    bt = torch.from_numpy(st.block_table).to(device)
+    scale = 1 / math.sqrt(c.head_dim)
+    out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale))
+    for b in [0, 9, 17, 31, 50, 63]:
+        rows = st.block_rows[b]
+        ids = torch.from_numpy(np.asarray(rows, np.int64)).to(device)
+        kb, vb = to_bits(kc[ids]), to_bits(vc[ids])
+        L = int(st.context_lens[b])
+        want = oracle.paged_decode_attention(
+            to_bits(q[b:b + 1]), kb, vb, np.array([0, L], np.uint32),
+            np.arange(len(rows), dtype=np.int32)[None], scale)
+        assert_attn_close(out[b:b + 1], want)

@@ -1,0 +1,224 @@
+"""Pins the C oracle (CPU only) against the reference's golden vectors, independent
+library routines (numpy, torch, python-xxhash) and closed forms.  Each test names
+what a plausible oracle mistake would break."""
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle
+from helpers import normal_bits
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_known_answers.json").read_text())
+
+
+# ------------------------------------------------------------------ formats
+def test_bf16_rounding_matches_torch():
+    import torch
+
+    rng = np.random.default_rng(0)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * 10 ** rng.uniform(-30, 30, 20000).astype(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, 1.0 + 2**-8, 1.0 + 3 * 2**-8, 3.3895e38, 1e-40],
+                 dtype=np.float32)])
+    want = torch.from_numpy(x).bfloat16().view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(oracle.float_to_half(x, "bf16"), want)
+    assert np.array_equal(oracle.f32_to_bf16_bits(x[np.isfinite(x)]), want[np.isfinite(x)])
+    back = oracle.half_to_float(want, "bf16")
+    assert np.array_equal(back.view(np.uint32), (want.astype(np.uint32) << 16))
+
+
+def test_f16_rounding_matches_numpy():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(20000).astype(np.float32) * np.float32(2.0) ** rng.integers(-30, 18, 20000).astype(np.float32),
+        np.array([0.0, -0.0, np.inf, -np.inf, 65504, 65519.99, 65520, 2**-24, 2**-25, 3 * 2**-26,
+                  2**-14 - 2**-25, 1e-8], dtype=np.float32)])
+    want = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(oracle.float_to_half(x, "f16"), want)
+    allbits = np.arange(65536, dtype=np.uint16)
+    ok = ~np.isnan(allbits.view(np.float16))
+    got = oracle.half_to_float(allbits, "f16")
+    assert np.array_equal(got[ok], allbits[ok].view(np.float16).astype(np.float32))
+
+
+# --------------------------------------------------------------- host logic
+@pytest.mark.parametrize("case", GOLDEN["slot_mapping"], ids=lambda c: c["cite"].split()[-1])
+def test_slot_mapping_reference_known_answers(case):
+    got = oracle.compute_slot_mapping(case["block_table"], case["block_size"], case["token_offset"],
+                                      case["num_tokens"])
+    assert got.tolist() == case["expected"]
+
+
+def test_slot_mapping_full_range():
+    c = GOLDEN["slot_mapping_full_range"]
+    got = oracle.compute_slot_mapping(c["block_table"], c["block_size"], 0, c["num_tokens"])
+    bt = c["block_table"]
+    assert got.tolist() == [bt[i // 256] * 256 + i % 256 for i in range(c["num_tokens"])]
+
+
+@pytest.mark.parametrize("case", GOLDEN["decode_metadata"], ids=lambda c: c["cite"].split()[-1])
+def test_decode_metadata_reference_known_answers(case):
+    cu_q, cu_k, mx = oracle.build_decode_metadata(case["context_lens"])
+    assert cu_q.tolist() == case["cu_seqlens_q"]
+    assert cu_k.tolist() == case["cu_seqlens_k"]
+    assert mx == case["max_seqlen_k"]
+
+
+def test_pad_block_table():
+    rows = [[7, 3], [], [1, 2, 9, 4], [5]]
+    got = oracle.pad_block_table(rows)
+    assert got.tolist() == [[7, 3, 0, 0], [0, 0, 0, 0], [1, 2, 9, 4], [5, 0, 0, 0]]
+
+
+# ------------------------------------------------------------ cache copies
+def test_reshape_and_cache_reference_known_answer():
+    ka = GOLDEN["reshape_and_cache_known_answer"]
+    T, H, D, NB, BS = ka["num_tokens"], ka["num_kv_heads"], ka["head_dim"], ka["num_blocks"], ka["block_size"]
+    key = oracle.f32_to_bf16_bits(np.arange(T * H * D, dtype=np.float32)).reshape(T, H, D)
+    val = oracle.f32_to_bf16_bits(1000 + np.arange(T * H * D, dtype=np.float32)).reshape(T, H, D)
+    kc = np.zeros((NB, BS, H, D), np.uint16)
+    vc = np.zeros_like(kc)
+    oracle.reshape_and_cache(key, val, kc, vc, np.array(ka["slot_mapping"], np.int64))
+    assert np.array_equal(kc[0, 0], key[0]) and np.array_equal(kc[1, 0], key[1])
+    assert np.array_equal(vc[2, 0], val[2])
+    assert np.count_nonzero(kc) == np.count_nonzero(key)
+
+
+def test_reshape_and_cache_matches_fancy_index_and_skips_minus_one():
+    rng = np.random.default_rng(3)
+    NB, BS, H, D, T = 5, 16, 2, 8, 40
+    kc = rng.integers(0, 65535, (NB, BS, H, D)).astype(np.uint16)
+    vc = rng.integers(0, 65535, (NB, BS, H, D)).astype(np.uint16)
+    key = rng.integers(0, 65535, (T, H, D)).astype(np.uint16)
+    val = rng.integers(0, 65535, (T, H, D)).astype(np.uint16)
+    slots = rng.choice(NB * BS, T, replace=False).astype(np.int64)
+    slots[3::5] = -1
+    ek, ev = kc.copy().reshape(-1, H, D), vc.copy().reshape(-1, H, D)
+    keep = slots >= 0
+    ek[slots[keep]] = key[keep]
+    ev[slots[keep]] = val[keep]
+    oracle.reshape_and_cache(key, val, kc, vc, slots)
+    assert np.array_equal(kc.reshape(-1, H, D), ek) and np.array_equal(vc.reshape(-1, H, D), ev)
+
+
+def test_copy_and_gather_match_fancy_index():
+    rng = np.random.default_rng(4)
+    kc = rng.integers(0, 2**32, (8, 4, 3, 5), dtype=np.uint64).astype(np.uint32)
+    vc = rng.integers(0, 2**32, (8, 4, 3, 5), dtype=np.uint64).astype(np.uint32)
+    mapping = np.array([[0, 5], [2, 6], [3, 3]], np.int64)
+    ek, ev = kc.copy(), vc.copy()
+    ek[mapping[:, 1]] = kc[mapping[:, 0]]
+    ev[mapping[:, 1]] = vc[mapping[:, 0]]
+    oracle.copy_blocks(kc, vc, mapping)
+    assert np.array_equal(kc, ek) and np.array_equal(vc, ev)
+    ids = np.array([7, 0, 6], np.int32)
+    gk, gv = oracle.gather_blocks(kc, vc, ids)
+    assert np.array_equal(gk, kc[ids]) and np.array_equal(gv, vc[ids])
+
+
+# --------------------------------------------------------------- attention
+def _rand_case(seed, B, Hq, Hkv, D, BS, NB, lens, dtype="bf16"):
+    rng = np.random.default_rng(seed)
+    lens = np.asarray(lens)
+    nblk = (lens + BS - 1) // BS
+    perm = rng.permutation(NB).astype(np.int32)
+    table = np.zeros((B, max(int(nblk.max()), 1)), np.int32)
+    pos = 0
+    for b in range(B):
+        table[b, :nblk[b]] = perm[pos:pos + nblk[b]]
+        pos += nblk[b]
+    cu = np.zeros(B + 1, np.uint32)
+    cu[1:] = np.cumsum(lens)
+    return (normal_bits(rng, (B, Hq, D), dtype), normal_bits(rng, (NB, BS, Hkv, D), dtype),
+            normal_bits(rng, (NB, BS, Hkv, D), dtype), cu, table)
+
+
+def _numpy_f64_attention(q, kc, vc, cu, table, scale, window, dtype):
+    """Independent textbook routine: gather contiguous K/V with numpy fancy indexing,
+    then softmax(scale q K^T) V in float64."""
+    B, Hq, D = q.shape
+    NB, BS, Hkv, _ = kc.shape
+    G = Hq // Hkv
+    qf = oracle.bits_to_f32(q, dtype).astype(np.float64)
+    kf = oracle.bits_to_f32(kc, dtype).astype(np.float64)
+    vf = oracle.bits_to_f32(vc, dtype).astype(np.float64)
+    out = np.zeros((B, Hq, D))
+    for b in range(B):
+        L = int(cu[b + 1] - cu[b])
+        if L == 0:
+            continue
+        j = np.arange(L)
+        rows = table[b, j // BS].astype(np.int64) * BS + j % BS
+        K = kf.reshape(-1, Hkv, D)[rows]  # [L, Hkv, D]
+        V = vf.reshape(-1, Hkv, D)[rows]
+        lo = 0 if window < 0 else max(0, L - 1 - window)
+        for h in range(Hq):
+            s = K[lo:, h // G] @ qf[b, h] * scale
+            p = np.exp(s - s.max())
+            out[b, h] = (p / p.sum()) @ V[lo:, h // G]
+    return out
+
+
+@pytest.mark.parametrize("G,D,BS,window,dtype", [(2, 128, 256, -1, "bf16"), (4, 128, 16, 37, "bf16"),
+                                                 (1, 64, 32, -1, "f16"), (8, 64, 256, 300, "f16")])
+def test_attention_matches_numpy_f64(G, D, BS, window, dtype):
+    Hkv = 2
+    q, kc, vc, cu, table = _rand_case(5, 3, G * Hkv, Hkv, D, BS, 80, [700, 1, 0], dtype)
+    scale = 1 / math.sqrt(D)
+    want = _numpy_f64_attention(q, kc, vc, cu, table, scale, window, dtype)
+    got32 = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype)
+    got64 = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype, use_f64=True)
+    np.testing.assert_allclose(got64, want, atol=1e-7, rtol=1e-6)  # fp32 output rounding
+    np.testing.assert_allclose(got32, want, atol=2e-5, rtol=1e-4)
+    # Wrong kv-head mapping (h % Hkv instead of h // G) must be caught: heads differ.
+    assert not np.allclose(want[0, 0], want[0, -1])
+
+
+def test_attention_closed_forms():
+    q, kc, vc, cu, table = _rand_case(6, 2, 8, 2, 64, 16, 40, [100, 1])
+    scale = 0.125
+    # L = 1: output is v_0 exactly.
+    out = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, -1, "bf16")
+    v0 = oracle.bits_to_f32(vc[table[1, 0], 0], "bf16")
+    assert np.array_equal(out[1], np.repeat(v0, 4, axis=0))
+    # q = 0: uniform weights -> mean of V over the window.
+    qz = np.zeros_like(q)
+    out = oracle.paged_decode_attention(qz, kc, vc, cu, table, scale, 9, "bf16")
+    j = np.arange(90, 100)
+    rows = table[0, j // 16].astype(np.int64) * 16 + j % 16
+    Vw = oracle.bits_to_f32(vc.reshape(-1, 2, 64)[rows], "bf16")
+    np.testing.assert_allclose(out[0, :4], np.repeat(Vw[:, 0].mean(0)[None], 4, 0), atol=1e-6)
+    np.testing.assert_allclose(out[0, 4:], np.repeat(Vw[:, 1].mean(0)[None], 4, 0), atol=1e-6)
+    # A huge score on one key: output is that key's V row.
+    kc2 = np.zeros_like(kc)
+    blk, off = table[0, 3], 5  # key 53
+    kc2[blk, off, 0] = oracle.f32_to_bf16_bits(np.full(64, 8.0, np.float32))
+    q1 = oracle.f32_to_bf16_bits(np.full(q.shape, 8.0, np.float32))
+    out = oracle.paged_decode_attention(q1, kc2, vc, cu, table, 1.0, -1, "bf16")
+    np.testing.assert_allclose(out[0, 0], oracle.bits_to_f32(vc[blk, off, 0], "bf16"), atol=1e-6)
+
+
+def test_attention_window_edge_counts_w_plus_one_keys():
+    """window_left = w admits keys [L-1-w, L-1]: w + 1 keys (FA2 convention)."""
+    q, kc, vc, cu, table = _rand_case(7, 1, 2, 1, 64, 16, 10, [50])
+    qz = np.zeros_like(q)
+    out = oracle.paged_decode_attention(qz, kc, vc, cu, table, 1.0, 2, "bf16")
+    j = np.array([47, 48, 49])
+    rows = table[0, j // 16].astype(np.int64) * 16 + j % 16
+    want = oracle.bits_to_f32(vc.reshape(-1, 1, 64)[rows, 0], "bf16").mean(0)
+    np.testing.assert_allclose(out[0, 0], want, atol=1e-6)
+
+
+# ------------------------------------------------------------------- xxh64
+def test_xxh64_matches_python_xxhash():
+    import xxhash
+
+    rng = np.random.default_rng(8)
+    assert oracle.xxh64(b"", 0) == 0xEF46DB3751D8E999  # spec's empty-input digest
+    for n in [0, 1, 3, 4, 7, 8, 31, 32, 33, 63, 64, 100, 1027]:
+        data = rng.integers(0, 256, n).astype(np.uint8).tobytes()
+        for seed in (0, 1, 2**63 + 5):
+            assert oracle.xxh64(data, seed) == xxhash.xxh64_intdigest(data, seed=seed)

@@ -1,0 +1,68 @@
+"""Builds liboxide_paged_kv.so (gfx950 HIP kernels + C ABI + C++ host layer).
+
+The library is built in-tree, next to this file, with plain hipcc calls (no
+cmake, no JIT cache), so the .so travels with the source tree.  Every call
+recompiles.  Counterpart of the reference's crates/vllm-oxide/build.rs:1-30
+(nvcc via cudaforge -> static lib); here hipcc --offload-arch=gfx950 -> shared
+lib that Python loads with ctypes and a Rust crate would link.
+"""
+from __future__ import annotations
+
+import os
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+REPO = PKG.parent
+CSRC = PKG / "csrc"
+HOST = PKG / "host"
+INCLUDE = REPO / "include"
+BUILD = PKG / "_build"
+LIB = PKG / "liboxide_paged_kv.so"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+ARCH = "gfx950"
+
+# -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in any kernel.
+HIP_FLAGS = [
+    "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall", "-Wno-unused-function",
+]
+
+
+def _sources() -> list[Path]:
+    return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp")) + sorted(HOST.glob("*.cpp"))
+
+
+def _compile(src: Path) -> Path:
+    obj = BUILD / (src.parent.name + "_" + src.stem + ".o")
+    cmd = [HIPCC, *HIP_FLAGS, "-I", str(INCLUDE), "-I", str(CSRC), "-I", str(HOST)]
+    if src.suffix == ".cpp":
+        cmd += ["-x", "hip"]
+    cmd += ["-c", str(src), "-o", str(obj)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
+    return obj
+
+
+def build(verbose: bool = False) -> Path:
+    BUILD.mkdir(exist_ok=True)
+    srcs = _sources()
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(_compile, srcs))
+    cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(LIB), *map(str, objs)]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    if verbose:
+        print(f"built {LIB}")
+    return LIB
+
+
+if __name__ == "__main__":
+    build(verbose=True)
+    sys.exit(0)

@@ -1,0 +1,176 @@
+// Whole-block copies inside the paged cache: copy_blocks (prefix-cache
+// copy-on-write) and gather_blocks (prefix-hit gather into a contiguous run).
+//
+// copy_blocks follows crates/vllm-oxide/kernels/copy_blocks.cu:8-28 (for pair
+// p: block dst of both caches becomes block src) and its C entry :30-61
+// (same symbol and parameters; block_stride in elements).  gather_blocks has
+// no reference counterpart and reuses the same machinery with a contiguous
+// destination.
+//
+// gfx950 design: a block of Qwen3-8B K (256 tokens x 8 heads x 128 x bf16) is
+// 512 KiB, so a pair is pure HBM streaming.  Each workgroup owns one pair and
+// a 16 KiB slice of it (256 lanes x 4 x 128-bit vectors) and moves the slice
+// of K and of V, keeping 8 independent 128-bit loads in flight per lane before
+// the stores.  blockIdx.x walks pairs, blockIdx.y walks slices, so a launch
+// has pairs x (block_bytes / 16 KiB) workgroups: 4096 for 128 pairs of 512 KiB,
+// enough to cover all 256 CUs many times over.  The copy is bitwise, so every
+// dtype takes the same path; strides that are not a multiple of 16 bytes fall
+// back to a per-element copy.
+#include "oxide_common.hpp"
+
+namespace {
+
+using oxide::u32x4;
+
+constexpr int kThreads = 256;
+constexpr int kUnroll = 4;
+constexpr int64_t kVecsPerGroup = kThreads * kUnroll;
+
+// src/dst block ids for workgroup row `p`.  mode 0: block_mapping int64 [P,2]
+// (src, dst) inside one cache.  mode 1: gather, src = block_ids[p], dst = p.
+struct PairIds {
+  int64_t src, dst;
+};
+
+template <int kMode>
+__device__ __forceinline__ PairIds pair_ids(const void* ids, int64_t p) {
+  if (kMode == 0) {
+    const int64_t* m = static_cast<const int64_t*>(ids);
+    return {m[2 * p], m[2 * p + 1]};
+  } else {
+    const int32_t* b = static_cast<const int32_t*>(ids);
+    return {static_cast<int64_t>(b[p]), p};
+  }
+}
+
+template <int kMode>
+__global__ __launch_bounds__(kThreads) void block_copy_vec16(
+    const u32x4* __restrict__ k_src, const u32x4* __restrict__ v_src, u32x4* k_dst,
+    u32x4* v_dst, const void* __restrict__ ids, int64_t block_vecs) {
+  const PairIds pr = pair_ids<kMode>(ids, blockIdx.x);
+  const int64_t base = static_cast<int64_t>(blockIdx.y) * kVecsPerGroup + threadIdx.x;
+  const u32x4* ks = k_src + pr.src * block_vecs;
+  const u32x4* vs = v_src ? v_src + pr.src * block_vecs : nullptr;
+  u32x4* kd = k_dst + pr.dst * block_vecs;
+  u32x4* vd = v_dst ? v_dst + pr.dst * block_vecs : nullptr;
+  if (base + (kUnroll - 1) * kThreads < block_vecs) {
+    u32x4 kr[kUnroll], vr[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) kr[u] = __builtin_nontemporal_load(ks + base + u * kThreads);
+    if (vs) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        vr[u] = __builtin_nontemporal_load(vs + base + u * kThreads);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) kd[base + u * kThreads] = kr[u];
+    if (vs) {
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) vd[base + u * kThreads] = vr[u];
+    }
+  } else {
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t i = base + u * kThreads;
+      if (i < block_vecs) {
+        kd[i] = ks[i];
+        if (vs) vd[i] = vs[i];
+      }
+    }
+  }
+}
+
+template <int kMode, typename E>
+__global__ __launch_bounds__(kThreads) void block_copy_elem(const E* __restrict__ k_src,
+                                                            const E* __restrict__ v_src,
+                                                            E* k_dst, E* v_dst,
+                                                            const void* __restrict__ ids,
+                                                            int64_t block_elems) {
+  const PairIds pr = pair_ids<kMode>(ids, blockIdx.x);
+  const int64_t e = static_cast<int64_t>(blockIdx.y) * kThreads + threadIdx.x;
+  if (e >= block_elems) return;
+  k_dst[pr.dst * block_elems + e] = k_src[pr.src * block_elems + e];
+  if (v_src) v_dst[pr.dst * block_elems + e] = v_src[pr.src * block_elems + e];
+}
+
+template <int kMode>
+void launch_block_copy(const void* k_src, const void* v_src, void* k_dst, void* v_dst,
+                       const void* ids, int64_t num_rows, int64_t block_stride, int esize,
+                       hipStream_t s) {
+  const int64_t block_bytes = block_stride * esize;
+  const bool vec = block_bytes % 16 == 0 && oxide::aligned16(k_src) && oxide::aligned16(k_dst) &&
+                   (!v_src || (oxide::aligned16(v_src) && oxide::aligned16(v_dst)));
+  if (vec) {
+    const int64_t block_vecs = block_bytes / 16;
+    const dim3 grid(static_cast<unsigned>(num_rows),
+                    static_cast<unsigned>((block_vecs + kVecsPerGroup - 1) / kVecsPerGroup));
+    hipLaunchKernelGGL(block_copy_vec16<kMode>, grid, dim3(kThreads), 0, s,
+                       static_cast<const u32x4*>(k_src), static_cast<const u32x4*>(v_src),
+                       static_cast<u32x4*>(k_dst), static_cast<u32x4*>(v_dst), ids, block_vecs);
+  } else {
+    const dim3 grid(static_cast<unsigned>(num_rows),
+                    static_cast<unsigned>((block_stride + kThreads - 1) / kThreads));
+    if (esize == 2) {
+      hipLaunchKernelGGL((block_copy_elem<kMode, uint16_t>), grid, dim3(kThreads), 0, s,
+                         static_cast<const uint16_t*>(k_src), static_cast<const uint16_t*>(v_src),
+                         static_cast<uint16_t*>(k_dst), static_cast<uint16_t*>(v_dst), ids,
+                         block_stride);
+    } else {
+      hipLaunchKernelGGL((block_copy_elem<kMode, uint32_t>), grid, dim3(kThreads), 0, s,
+                         static_cast<const uint32_t*>(k_src), static_cast<const uint32_t*>(v_src),
+                         static_cast<uint32_t*>(k_dst), static_cast<uint32_t*>(v_dst), ids,
+                         block_stride);
+    }
+  }
+  oxide::check_launch();
+}
+
+bool rows_fit_grid(int64_t rows, int64_t block_stride) {
+  // gridDim.x holds the pair/block index; gridDim.y the slices of one block
+  // (at most 65535 slices: 1 GiB blocks on the vector path, 32 MiB on the
+  // per-element path).
+  return rows <= INT32_MAX && (block_stride + kThreads - 1) / kThreads <= 65535;
+}
+
+}  // namespace
+
+extern "C" void copy_blocks(void* key_cache, void* value_cache, const int64_t* block_mapping,
+                            int64_t num_pairs, int64_t block_stride, int dtype, void* stream) {
+  const int esize = oxide::dtype_size(dtype);
+  if (esize == 0) {
+    oxide::set_error(OXIDE_ERR_UNSUPPORTED_DTYPE);
+    return;
+  }
+  if (num_pairs < 0 || block_stride < 0) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  if (num_pairs == 0 || block_stride == 0) return;
+  if (!key_cache || !value_cache || !block_mapping || !rows_fit_grid(num_pairs, block_stride)) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  launch_block_copy<0>(key_cache, value_cache, key_cache, value_cache, block_mapping, num_pairs,
+                       block_stride, esize, oxide::as_stream(stream));
+}
+
+extern "C" void gather_blocks(void* key_dst, void* value_dst, const void* key_cache,
+                              const void* value_cache, const int32_t* block_ids,
+                              int64_t num_blocks, int64_t block_stride, int dtype, void* stream) {
+  const int esize = oxide::dtype_size(dtype);
+  if (esize == 0) {
+    oxide::set_error(OXIDE_ERR_UNSUPPORTED_DTYPE);
+    return;
+  }
+  if (num_blocks < 0 || block_stride < 0) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  if (num_blocks == 0 || block_stride == 0) return;
+  if (!key_dst || !key_cache || !block_ids || (value_dst == nullptr) != (value_cache == nullptr) ||
+      !rows_fit_grid(num_blocks, block_stride)) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  launch_block_copy<1>(key_cache, value_cache, key_dst, value_dst, block_ids, num_blocks,
+                       block_stride, esize, oxide::as_stream(stream));
+}

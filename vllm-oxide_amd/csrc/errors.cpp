@@ -1,0 +1,42 @@
+// Per-host-thread error state behind oxide_last_error().  The reference's entry
+// points return void and drop launch errors (reshape_and_cache.cu:30,
+// copy_blocks.cu:30); this library keeps the void ABI and makes the failure
+// queryable instead.
+#include "oxide_common.hpp"
+
+namespace oxide {
+
+static thread_local int g_last_error = OXIDE_OK;
+
+void set_error(int code) {
+  if (g_last_error == OXIDE_OK) g_last_error = code;
+}
+
+void check_launch() {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) set_error(OXIDE_ERR_HIP + static_cast<int>(e));
+}
+
+}  // namespace oxide
+
+extern "C" int oxide_last_error(void) { return oxide::g_last_error; }
+
+extern "C" void oxide_clear_error(void) { oxide::g_last_error = OXIDE_OK; }
+
+extern "C" const char* oxide_error_string(int code) {
+  switch (code) {
+    case OXIDE_OK:
+      return "ok";
+    case OXIDE_ERR_INVALID_ARGUMENT:
+      return "invalid argument";
+    case OXIDE_ERR_UNSUPPORTED_DTYPE:
+      return "unsupported dtype code";
+    case OXIDE_ERR_UNSUPPORTED_SHAPE:
+      return "unsupported shape (head_dim, group size or block size)";
+    case OXIDE_ERR_WORKSPACE_TOO_SMALL:
+      return "workspace too small";
+    default:
+      if (code > OXIDE_ERR_HIP) return hipGetErrorString(static_cast<hipError_t>(code - OXIDE_ERR_HIP));
+      return "unknown error";
+  }
+}

@@ -1,0 +1,9 @@
+"""MI355X (gfx950) paged-KV hot path of vllm-oxide: Python front end.
+
+The kernels live in liboxide_paged_kv.so (HIP, built in-tree by
+vllm-oxide_amd/build.py); this package only binds them (ctypes) and generates
+the synthetic workloads of the benchmark configurations.
+"""
+from ._lib import LIB_PATH, OxideError, load  # noqa: F401
+from .ops import (copy_blocks, decode_attn, dtype_code, gather_blocks,  # noqa: F401
+                  reshape_and_cache, split_tokens, workspace_size)

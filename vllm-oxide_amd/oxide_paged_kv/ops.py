@@ -1,0 +1,133 @@
+"""torch-tensor front end of the C ABI, shaped like the reference's Rust wrappers.
+
+* reshape_and_cache / copy_blocks mirror crates/vllm-oxide/src/attention/kernels.rs:106-180
+  (dims taken from the tensors, dtype code from the key dtype, the tensor's stream).
+* decode_attn mirrors flash_attn_varlen_paged_windowed as called at
+  crates/vllm-oxide/src/attention/flash_attn.rs:39-68 (the callee allocates the output).
+* gather_blocks is the prefix-hit gather (no reference counterpart).
+
+Tensors must be contiguous CUDA (HIP) tensors; every call goes to the HIP library
+on torch's current stream and raises OxideError if the library reports an error.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_DTYPE_CODE = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16,
+               torch.float32: _lib.DTYPE_F32}
+
+
+def dtype_code(dt: torch.dtype) -> int:
+    """kernels.rs:97-104: f16 -> 0, bf16 -> 1, f32 -> 2; anything else is an error."""
+    try:
+        return _DTYPE_CODE[dt]
+    except KeyError:
+        raise _lib.OxideError(f"unsupported KV cache dtype: {dt}") from None
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise _lib.OxideError("expected a device tensor")
+    if not t.is_contiguous():
+        raise _lib.OxideError("expected a contiguous tensor")
+    return t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def reshape_and_cache(key: torch.Tensor, value: torch.Tensor, key_cache: torch.Tensor,
+                      value_cache: torch.Tensor, slot_mapping: torch.Tensor) -> None:
+    """Append: key/value [T, Hkv, D] into the per-layer caches [NB, BS, Hkv, D] at slot_mapping (int64)."""
+    L = _lib.load()
+    if slot_mapping.dtype != torch.int64:
+        raise _lib.OxideError("slot_mapping must be int64")
+    T, H, D = key.shape
+    L.reshape_and_cache(_ptr(key), _ptr(value), _ptr(key_cache), _ptr(value_cache),
+                        _ptr(slot_mapping), T, H, D, dtype_code(key.dtype), _stream(key))
+    _lib.check()
+
+
+def copy_blocks(key_cache: torch.Tensor, value_cache: torch.Tensor,
+                block_mapping: torch.Tensor) -> None:
+    """Copy-on-write: block_mapping int64 [P, 2] of (src, dst) block ids."""
+    L = _lib.load()
+    if block_mapping.dtype != torch.int64:
+        raise _lib.OxideError("block_mapping must be int64")
+    num_pairs = block_mapping.shape[0]
+    d = key_cache.shape
+    block_stride = d[1] * d[2] * d[3]  # kernels.rs:164-165
+    L.copy_blocks(_ptr(key_cache), _ptr(value_cache), _ptr(block_mapping), num_pairs, block_stride,
+                  dtype_code(key_cache.dtype), _stream(key_cache))
+    _lib.check()
+
+
+def gather_blocks(key_cache: torch.Tensor, value_cache: torch.Tensor | None,
+                  block_ids: torch.Tensor, key_out: torch.Tensor | None = None,
+                  value_out: torch.Tensor | None = None):
+    """Prefix-hit gather: returns contiguous [n * BS, Hkv, D] K (and V) of the listed blocks."""
+    L = _lib.load()
+    if block_ids.dtype != torch.int32:
+        raise _lib.OxideError("block_ids must be int32")
+    n = block_ids.shape[0]
+    NB, BS, H, D = key_cache.shape
+    if key_out is None:
+        key_out = torch.empty((n * BS, H, D), dtype=key_cache.dtype, device=key_cache.device)
+    if value_cache is not None and value_out is None:
+        value_out = torch.empty_like(key_out)
+    L.gather_blocks(_ptr(key_out), _ptr(value_out) if value_cache is not None else None,
+                    _ptr(key_cache), _ptr(value_cache), _ptr(block_ids), n, BS * H * D,
+                    dtype_code(key_cache.dtype), _stream(key_cache))
+    _lib.check()
+    return key_out, value_out
+
+
+def workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                   max_seqlen_k: int) -> int:
+    return int(_lib.load().paged_decode_attention_workspace_size(batch, num_heads, num_kv_heads,
+                                                                 head_dim, max_seqlen_k))
+
+
+def split_tokens(batch: int, num_kv_heads: int, max_seqlen_k: int) -> int:
+    return int(_lib.load().paged_decode_attention_split_tokens(batch, num_kv_heads, max_seqlen_k))
+
+
+def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                cu_seqlens_k: torch.Tensor, block_table: torch.Tensor, max_seqlen_k: int,
+                softmax_scale: float, window_left: int | None = None,
+                page_block_size: int = 256, out: torch.Tensor | None = None,
+                workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """Paged decode attention.
+
+    q [B, Hq, D]; k_cache/v_cache [NB, page_block_size, Hkv, D]; cu_seqlens_k uint32-valued
+    int32 tensor [B + 1] (torch has no uint32 arithmetic; the bits are passed as is);
+    block_table int32 [B, max_blocks] padded with 0; window_left None = unbounded.
+    """
+    L = _lib.load()
+    B, Hq, D = q.shape
+    NB, BS, Hkv, D2 = k_cache.shape
+    if D2 != D or BS != page_block_size or v_cache.shape != k_cache.shape:
+        raise _lib.OxideError("q / k_cache / v_cache shapes disagree")
+    if block_table.dtype != torch.int32 or cu_seqlens_k.dtype not in (torch.int32, torch.uint32):
+        raise _lib.OxideError("block_table must be int32 and cu_seqlens_k 32-bit")
+    if k_cache.dtype != q.dtype or v_cache.dtype != q.dtype:
+        raise _lib.OxideError("q and caches must share a dtype")
+    if out is None:
+        out = torch.empty_like(q)
+    need = workspace_size(B, Hq, Hkv, D, max_seqlen_k)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    max_blocks = block_table.shape[1] if block_table.dim() == 2 else 0
+    L.paged_decode_attention(
+        _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k), _ptr(block_table),
+        max_blocks, NB, B, Hq, Hkv, D, BS, max_seqlen_k,
+        -1 if window_left is None else int(window_left), float(softmax_scale),
+        _ptr(workspace), workspace.numel() * workspace.element_size(), dtype_code(q.dtype),
+        _stream(q))
+    _lib.check()
+    return out
