@@ -49,6 +49,32 @@ typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
+// Build-time tuning knobs (defaults are the tuned values).
+#ifndef OXIDE_SPLIT_TOKENS
+#define OXIDE_SPLIT_TOKENS 0  // 0 = policy in choose_split_tokens
+#endif
+#ifndef OXIDE_DECODE_WAVES_PER_EU
+#define OXIDE_DECODE_WAVES_PER_EU 0  // >0: ask the compiler for this occupancy
+#endif
+#if OXIDE_DECODE_WAVES_PER_EU > 0
+#define OXIDE_DECODE_OCCUPANCY __attribute__((amdgpu_waves_per_eu(OXIDE_DECODE_WAVES_PER_EU)))
+#else
+#define OXIDE_DECODE_OCCUPANCY
+#endif
+#ifndef OXIDE_KV_NONTEMPORAL
+#define OXIDE_KV_NONTEMPORAL 1  // 1 = K/V streamed with non-temporal loads
+#endif
+
+// One 16-byte K/V chunk.
+__device__ __forceinline__ uint4 load_kv16(const uint16_t* p) {
+#if OXIDE_KV_NONTEMPORAL
+  const oxide::u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const oxide::u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *reinterpret_cast<const uint4*>(p);
+#endif
+}
+
 struct Bf16Tag {};
 struct F16Tag {};
 
@@ -136,16 +162,20 @@ __device__ __forceinline__ int seq_len(const DecodeParams& p, int b) {
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 
-template <class Tag, int D, int G, int NT>
-__global__ __launch_bounds__(kThreads) void paged_decode_split(DecodeParams p) {
+template <class Tag, int D, int G, int TILES>
+__global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_split(DecodeParams p) {
   constexpr int KK = D / 32;     // MFMA k-steps per key row
   constexpr int CH = D / 8;      // 16-byte chunks per row
-  constexpr int RPL = 64 / CH;   // V rows per wave-wide load
-  constexpr int VL = 16 / RPL;   // V loads per 16-key tile
-  constexpr int BT = 16 * NT;    // keys per wave batch
+  constexpr int RPL = 64 / CH;   // rows per wave-wide K/V load
+  constexpr int VL = 16 / RPL;   // K (and V) loads per 16-key tile
   constexpr int GP = G < 4 ? 4 : G;  // padded LDS row (floats) for 16-byte reads
+  constexpr int WT = 16 * TILES;     // keys per wave; split = kWaves * WT
 
-  __shared__ __align__(16) float s_p[kWaves][NT][16][GP];
+  // K tile in MFMA order: row r holds 16-byte chunk c at slot c ^ (r % CH),
+  // which keeps both the row-wise writes and the column-wise MFMA reads
+  // spread over all LDS banks.
+  __shared__ __align__(16) uint4 s_k[kWaves][16][CH];
+  __shared__ __align__(16) float s_p[kWaves][16][GP];
   __shared__ __align__(16) float s_alpha[kWaves][GP];
   __shared__ __align__(16) float s_o[kWaves][G][D];
   __shared__ float s_m[kWaves][G];
@@ -156,8 +186,8 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split(DecodeParams p) {
   const int b = blockIdx.z;
   const int L = seq_len(p, b);
   const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
-  const int s0 = split * p.split_tokens;
-  if (s0 >= L || s0 + p.split_tokens <= lo) return;  // the merge skips exactly these splits
+  const int s0 = split * (kWaves * WT);
+  if (s0 >= L || s0 + kWaves * WT <= lo) return;  // the merge skips exactly these splits
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -165,24 +195,17 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split(DecodeParams p) {
   const int grp = lane >> 4;
   const int vch = lane % CH;
   const int vrow = lane / CH;
-  const int wt = p.split_tokens / kWaves;
-  // This wave's keys: [a, e).  Wave-uniform, so kept in scalar registers.
-  const int a = __builtin_amdgcn_readfirstlane(max(lo, s0 + wave * wt));
-  const int e = __builtin_amdgcn_readfirstlane(min(L, s0 + (wave + 1) * wt));
+  // This wave's keys: [a, e) inside its region [w0, w0 + WT).  Wave-uniform.
+  const int w0 = s0 + wave * WT;
+  const int a = __builtin_amdgcn_readfirstlane(max(lo, w0));
+  const int e = __builtin_amdgcn_readfirstlane(min(L, w0 + WT));
 
   const int BS = p.block_size;
   const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;  // elements per key row
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + kh * D;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + kh * D;
   const int32_t* bt = p.block_table + b * p.max_blocks;
-
-  // A operand: query (r16 % G) of this kv head's group, chunk grp + 4*kk.
   const int qh0 = kh * G;
-  const uint16_t* qrow =
-      static_cast<const uint16_t*>(p.q) + (static_cast<int64_t>(b) * p.num_heads + qh0 + r16 % G) * D;
-  uint4 qa[KK];
-#pragma unroll
-  for (int kk = 0; kk < KK; ++kk) qa[kk] = *reinterpret_cast<const uint4*>(qrow + 8 * (grp + 4 * kk));
 
   float m_run[4], l_run[4];
 #pragma unroll
@@ -199,98 +222,102 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split(DecodeParams p) {
   // Lanes that own LDS probability columns: C rows 4*grp+j with 4*grp+j < G.
   const bool writer = 4 * grp < G;
 
-  for (int tb = a & ~15; tb < e; tb += BT) {
-    uint4 kr[NT][KK];
-    uint4 vr[NT][VL];
+  if (a < e) {
+    // A operand: query (r16 % G) of this kv head's group, chunk grp + 4*kk.
+    const uint16_t* qrow = static_cast<const uint16_t*>(p.q) +
+                           (static_cast<int64_t>(b) * p.num_heads + qh0 + r16 % G) * D;
+    uint4 qa[KK];
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int tt = tb + 16 * t;
-      if (tt < e) {
-        // Block ids outside [0, num_blocks) are clamped: the output is then
-        // meaningless but no access leaves the cache.
-        const int blk = min(max(bt[tt / BS], 0), p.num_blocks - 1);
-        const int64_t row0 = static_cast<int64_t>(blk) * BS + tt % BS;
-        const uint16_t* kp = kbase + (row0 + r16) * row_stride + 8 * grp;
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) kr[t][kk] = *reinterpret_cast<const uint4*>(kp + 32 * kk);
-        const uint16_t* vp = vbase + (row0 + vrow) * row_stride + 8 * vch;
-#pragma unroll
-        for (int j = 0; j < VL; ++j)
-          vr[t][j] = *reinterpret_cast<const uint4*>(vp + RPL * j * row_stride);
-      } else {
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) kr[t][kk] = make_uint4(0, 0, 0, 0);
-#pragma unroll
-        for (int j = 0; j < VL; ++j) vr[t][j] = make_uint4(0, 0, 0, 0);
-      }
-    }
+    for (int kk = 0; kk < KK; ++kk)
+      qa[kk] = *reinterpret_cast<const uint4*>(qrow + 8 * (grp + 4 * kk));
 
-    // Scores of key (tb + 16t + r16) for C rows j, scaled to the log2 domain.
-    floatx4 s[NT];
+    // Tile t covers keys [w0 + 16t, w0 + 16t + 16).  Loads are clamped to the
+    // valid tiles [a & ~15, (e-1) & ~15] (a clamped tile re-reads one already
+    // fetched: an L2 hit) and the compute masks keys outside [a, e), so the
+    // whole walk is straight-line code: the next tile's K/V loads stay in
+    // flight while the current tile computes.
+    const int first_tile = a & ~15;
+    const int last_tile = (e - 1) & ~15;
+    uint4 kst[2][VL], vst[2][VL];
+    auto load_tile = [&](int t, uint4 (&kr)[VL], uint4 (&vr)[VL]) {
+      const int tt = __builtin_amdgcn_readfirstlane(min(max(w0 + 16 * t, first_tile), last_tile));
+      // Block ids outside [0, num_blocks) are clamped: the output is then
+      // meaningless but no access leaves the cache.
+      const int blk = min(max(bt[tt / BS], 0), p.num_blocks - 1);
+      const int64_t row0 = static_cast<int64_t>(blk) * BS + tt % BS;
+      // K and V alike: 16 lanes cover one 256-byte head row, RPL rows per
+      // instruction, the shape that streams at full HBM rate.
+      const uint16_t* kp = kbase + (row0 + vrow) * row_stride + 8 * vch;
+      const uint16_t* vp = vbase + (row0 + vrow) * row_stride + 8 * vch;
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      s[t] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < VL; ++j) kr[j] = load_kv16(kp + RPL * j * row_stride);
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) s[t] = mfma16x16x32(Tag{}, qa[kk], kr[t][kk], s[t]);
-    }
-    float bmax[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+      for (int j = 0; j < VL; ++j) vr[j] = load_kv16(vp + RPL * j * row_stride);
+    };
+
+    load_tile(0, kst[0], vst[0]);
 #pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int tok = tb + 16 * t + r16;
+    for (int t = 0; t < TILES; ++t) {
+      if (t + 1 < TILES) load_tile(t + 1, kst[(t + 1) & 1], vst[(t + 1) & 1]);
+      const uint4(&kr)[VL] = kst[t & 1];
+      const uint4(&vr)[VL] = vst[t & 1];
+      const int tt = w0 + 16 * t;
+
+      // K tile -> LDS (row vrow + RPL*j, chunk vch), read back in the MFMA B
+      // layout (key r16, chunk grp + 4*kk).  The strip is private to the wave
+      // and one wave's LDS operations complete in order.
+#pragma unroll
+      for (int j = 0; j < VL; ++j) {
+        const int row = vrow + RPL * j;
+        s_k[wave][row][vch ^ (row % CH)] = kr[j];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      // Scores of key tt + r16 for C rows j, in the log2 domain.
+      floatx4 sc = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk)
+        sc = mfma16x16x32(Tag{}, qa[kk], s_k[wave][r16][(grp + 4 * kk) ^ (r16 % CH)], sc);
+      const int tok = tt + r16;
       const bool valid = tok >= a && tok < e;
+      float alpha[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float x = valid ? s[t][j] * p.scale_log2 : -INFINITY;
-        s[t][j] = x;
-        bmax[j] = fmaxf(bmax[j], x);
+        const float x = valid ? sc[j] * p.scale_log2 : -INFINITY;
+        const float mnew = fmaxf(m_run[j], row16_max(x));
+        const float msafe = mnew == -INFINITY ? 0.f : mnew;
+        alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - msafe);
+        const float pr = __builtin_amdgcn_exp2f(x - msafe);
+        sc[j] = pr;
+        l_run[j] = l_run[j] * alpha[j] + pr;
+        m_run[j] = mnew;
       }
-    }
-    float alpha[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float mnew = fmaxf(m_run[j], row16_max(bmax[j]));
-      const float msafe = mnew == -INFINITY ? 0.f : mnew;
-      alpha[j] = exp2f(m_run[j] - msafe);
-      float psum = 0.f;
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
-        const float pr = exp2f(s[t][j] - msafe);
-        s[t][j] = pr;
-        psum += pr;
-      }
-      l_run[j] = l_run[j] * alpha[j] + psum;
-      m_run[j] = mnew;
-    }
-    if (writer) {
-#pragma unroll
-      for (int t = 0; t < NT; ++t) {
+      if (writer) {
         if (G >= 4) {
-          *reinterpret_cast<floatx4*>(&s_p[wave][t][r16][4 * grp]) = s[t];
+          *reinterpret_cast<floatx4*>(&s_p[wave][r16][4 * grp]) = sc;
         } else {
 #pragma unroll
-          for (int j = 0; j < G; ++j) s_p[wave][t][r16][j] = s[t][j];
+          for (int j = 0; j < G; ++j) s_p[wave][r16][j] = sc[j];
+        }
+        if (r16 == 0) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (4 * grp + j < G) s_alpha[wave][4 * grp + j] = alpha[j];
         }
       }
-      if (r16 == 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          if (4 * grp + j < G) s_alpha[wave][4 * grp + j] = alpha[j];
-      }
-    }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 
+      // PV on the VALU: this lane's V chunk (8 d values) for rows vrow + RPL*j.
 #pragma unroll
-    for (int q = 0; q < G; ++q) {
-      const float al = s_alpha[wave][q];
+      for (int q = 0; q < G; ++q) {
+        const float al = s_alpha[wave][q];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) acc[q][i] *= al;
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int tt = tb + 16 * t;
-      if (tt >= e) break;
+        for (int i = 0; i < 8; ++i) acc[q][i] *= al;
+      }
       const bool full = tt >= a && tt + 16 <= e;
 #pragma unroll
       for (int j = 0; j < VL; ++j) {
@@ -299,7 +326,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split(DecodeParams p) {
         if (G >= 4) {
 #pragma unroll
           for (int q4 = 0; q4 < G; q4 += 4) {
-            const floatx4 x = *reinterpret_cast<const floatx4*>(&s_p[wave][t][row][q4]);
+            const floatx4 x = *reinterpret_cast<const floatx4*>(&s_p[wave][row][q4]);
             pq[q4] = x[0];
             pq[q4 + 1] = x[1];
             pq[q4 + 2] = x[2];
@@ -307,14 +334,14 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split(DecodeParams p) {
           }
         } else {
 #pragma unroll
-          for (int q = 0; q < G; ++q) pq[q] = s_p[wave][t][row][q];
+          for (int q = 0; q < G; ++q) pq[q] = s_p[wave][row][q];
         }
-        uint4 w = vr[t][j];
+        uint4 w = vr[j];
         if (!full) {
-          // Keys outside [a, e) carry p = 0; zero their V so stale cache
-          // contents (possibly NaN) cannot leak in through 0 * NaN.
-          const int tok = tt + row;
-          if (tok < a || tok >= e) w = make_uint4(0, 0, 0, 0);
+          // Keys outside [a, e) carry p = 0; zero their V so stale or
+          // re-read cache contents (possibly NaN) cannot leak in via 0 * NaN.
+          const int vt = tt + row;
+          if (vt < a || vt >= e) w = make_uint4(0, 0, 0, 0);
         }
         float vf[8];
         unpack2(Tag{}, w.x, vf[0], vf[1]);
@@ -326,8 +353,8 @@ __global__ __launch_bounds__(kThreads) void paged_decode_split(DecodeParams p) {
 #pragma unroll
           for (int i = 0; i < 8; ++i) acc[q][i] = fmaf(pq[q], vf[i], acc[q][i]);
       }
+      __builtin_amdgcn_wave_barrier();
     }
-    __builtin_amdgcn_wave_barrier();
   }
 
   // Wave totals: sum l over the 16 keys of a row; sum acc over V rows.
@@ -425,15 +452,19 @@ int64_t choose_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq
   // 512-key splits keep the partials under 2% of the K/V bytes; fall back to
   // 256 when that would leave too few workgroups to fill 256 CUs.
   const int64_t wgs512 = batch * num_kv_heads * ceil_div(max_seqlen_k, 512);
+  if (OXIDE_SPLIT_TOKENS > 0) return OXIDE_SPLIT_TOKENS;
   return wgs512 >= 4096 ? 512 : 256;
 }
 
 template <class Tag, int D, int G>
 void launch_split(const DecodeParams& p, int64_t batch, hipStream_t s) {
-  constexpr int NT = 2;
   const dim3 grid(static_cast<unsigned>(p.max_splits), static_cast<unsigned>(p.num_kv_heads),
                   static_cast<unsigned>(batch));
-  hipLaunchKernelGGL((paged_decode_split<Tag, D, G, NT>), grid, dim3(kThreads), 0, s, p);
+  // split_tokens = kWaves * 16 * TILES.
+  if (p.split_tokens == 256)
+    hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 4>), grid, dim3(kThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 8>), grid, dim3(kThreads), 0, s, p);
 }
 
 template <class Tag, int D>

@@ -5,10 +5,12 @@ There is no fallback: if the HIP library is not built, importing the ops raises.
 from __future__ import annotations
 
 import ctypes
+import os
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent.parent
-LIB_PATH = PKG_DIR / "liboxide_paged_kv.so"
+# OXIDE_PAGED_KV_LIB points at another build of the same library (e.g. a tuning variant).
+LIB_PATH = Path(os.environ.get("OXIDE_PAGED_KV_LIB", PKG_DIR / "liboxide_paged_kv.so"))
 
 DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 OXIDE_OK = 0
