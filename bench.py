@@ -118,7 +118,7 @@ def main() -> int:
     cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(dev)
     bt = torch.from_numpy(st.block_table).to(dev)
     out = torch.empty((cfg.batch, cfg.num_heads, D), dtype=torch.bfloat16, device=dev)
-    ws = torch.empty(max(ox.workspace_size(cfg.batch, cfg.num_heads, H, D, st.max_seqlen_k), 1),
+    ws = torch.zeros(max(ox.workspace_size(cfg.batch, cfg.num_heads, H, D, st.max_seqlen_k), 1),
                      dtype=torch.uint8, device=dev)
     scale = 1 / math.sqrt(D)
     window = None if cfg.window_left < 0 else cfg.window_left
@@ -200,7 +200,7 @@ def main() -> int:
         "tokens_per_s": round(cfg.batch / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "paged_decode_split + paged_decode_merge (one attention call)",
+                     "kernel": "paged_decode_split (split-KV attention with fused merge)",
                      "algorithmic_bytes": attn_bytes},
         **extra,
     }

@@ -121,7 +121,9 @@ void gather_blocks(void* key_dst, void* value_dst, const void* key_cache, const 
  * L_b == 0 produces zeros.  Supported: dtype f16 or bf16, head_dim 64 or 128,
  * num_heads / num_kv_heads in {1, 2, 4, 8, 16}, page_block_size a positive
  * multiple of 16.  workspace must hold
- * paged_decode_attention_workspace_size(...) bytes for the same arguments.
+ * paged_decode_attention_workspace_size(...) bytes for the same arguments (no
+ * initialisation needed).  Calls that share a workspace must not overlap in
+ * time.
  */
 void paged_decode_attention(void* out, const void* q, const void* k_cache, const void* v_cache,
                             const uint32_t* cu_seqlens_k, const int32_t* block_table,

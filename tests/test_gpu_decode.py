@@ -171,3 +171,25 @@ def test_decode_cfg3_full_size_sampled(device):
             to_bits(q[b:b + 1]), kb, vb, np.array([0, L], np.uint32),
             np.arange(len(rows), dtype=np.int32)[None], scale)
         assert_attn_close(out[b:b + 1], want)
+
+
+def test_decode_workspace_reuse_across_shapes(device):
+    """One workspace serves several calls of different shapes (and holds the
+    previous call's partials): each result must equal the same call made with a
+    fresh workspace, bit for bit."""
+    import torch
+    import oxide_paged_kv as ox
+
+    cases = [(4, 32, 8, 128, 256, 64, [5000, 4097, 100, 4096]), (3, 16, 8, 128, 256, 30, [2000, 700, 101]),
+             (2, 64, 8, 128, 256, 80, [9000, 513])]
+    ws = torch.full((64 << 20,), 0x7F, dtype=torch.uint8, device=device)
+    for rep in range(2):
+        for i, (B, Hq, Hkv, D, BS, NB, lens) in enumerate(cases):
+            q, kc, vc, cu, table, mx = _case(20 + i, B, Hq, Hkv, D, BS, NB, lens)
+            args = (to_torch(q, "bf16", device), to_torch(kc, "bf16", device), to_torch(vc, "bf16", device),
+                    torch.from_numpy(cu.view(np.int32)).to(device), torch.from_numpy(table).to(device), mx,
+                    0.0883883)
+            shared = to_bits(ox.decode_attn(*args, workspace=ws))
+            fresh = to_bits(ox.decode_attn(*args))
+            torch.cuda.synchronize()
+            assert np.array_equal(shared, fresh), (rep, i)

@@ -40,6 +40,8 @@
 // 2 * Hq * (D+1) * 4 bytes per split (under 2% at split_tokens = 512).
 #include <math.h>
 
+#include <algorithm>
+
 #include "oxide_common.hpp"
 
 namespace {
@@ -60,6 +62,9 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 #define OXIDE_DECODE_OCCUPANCY __attribute__((amdgpu_waves_per_eu(OXIDE_DECODE_WAVES_PER_EU)))
 #else
 #define OXIDE_DECODE_OCCUPANCY
+#endif
+#ifndef OXIDE_GRID_MODE
+#define OXIDE_GRID_MODE 2  // workgroup -> (split, head, seq) order, see decode_work_item
 #endif
 #ifndef OXIDE_KV_NONTEMPORAL
 #define OXIDE_KV_NONTEMPORAL 1  // 1 = K/V streamed with non-temporal loads
@@ -148,6 +153,7 @@ struct DecodeParams {
   int window_left;
   int split_tokens;
   int max_splits;
+  int batch;
   float scale_log2;
 };
 
@@ -161,6 +167,37 @@ __device__ __forceinline__ int seq_len(const DecodeParams& p, int b) {
 
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
+constexpr int kXcds = 8;  // MI355X: workgroup i runs on XCD i % 8
+
+// Work item (split, kv head, sequence) of this workgroup; false for padding.
+//   mode 0: 3-D grid (split, head, seq), seq slowest.
+//   mode 1: 3-D grid (head, seq, split), split slowest.
+//   mode 2/3: 1-D grid, XCD-grouped: a unit u = (seq, split) is pinned to XCD
+//   u % 8 and its kv heads are consecutive workgroups there, so one XCD reads
+//   all head slices of the unit's token rows together; units are numbered
+//   split-major (2) or seq-major (3).
+__device__ __forceinline__ bool decode_work_item(const DecodeParams& p, int& split, int& kh, int& b) {
+#if OXIDE_GRID_MODE == 0
+  split = blockIdx.x; kh = blockIdx.y; b = blockIdx.z;
+  return true;
+#elif OXIDE_GRID_MODE == 1
+  kh = blockIdx.x; b = blockIdx.y; split = blockIdx.z;
+  return true;
+#else
+  const int i = blockIdx.x;
+  const int j = i / kXcds;
+  kh = j % p.num_kv_heads;
+  const int u = (j / p.num_kv_heads) * kXcds + i % kXcds;
+  const int units = p.batch * p.max_splits;
+  if (u >= units) return false;
+#if OXIDE_GRID_MODE == 2
+  b = u % p.batch; split = u / p.batch;
+#else
+  split = u % p.max_splits; b = u / p.max_splits;
+#endif
+  return true;
+#endif
+}
 
 template <class Tag, int D, int G, int TILES>
 __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_split(DecodeParams p) {
@@ -181,13 +218,12 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
   __shared__ float s_m[kWaves][G];
   __shared__ float s_l[kWaves][G];
 
-  const int split = blockIdx.x;
-  const int kh = blockIdx.y;
-  const int b = blockIdx.z;
+  int split, kh, b;
+  if (!decode_work_item(p, split, kh, b)) return;
   const int L = seq_len(p, b);
   const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
   const int s0 = split * (kWaves * WT);
-  if (s0 >= L || s0 + kWaves * WT <= lo) return;  // the merge skips exactly these splits
+  if (s0 >= L || s0 + kWaves * WT <= lo) return;  // not one of this sequence's splits
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -387,6 +423,11 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
   }
   __syncthreads();
 
+  // Combine the 4 waves: normalised split output o and its log2-sum-exp.
+  const int first = lo / (kWaves * WT);
+  const int nsplits = (L - 1) / (kWaves * WT) - first + 1;
+  uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + qh0) * D;
+  const int64_t prow0 = (static_cast<int64_t>(b) * p.num_heads + qh0) * p.max_splits;
   for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
     const int q = idx / D;
     const int d = idx % D;
@@ -397,17 +438,24 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
     float lsum = 0.f, osum = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float f = exp2f(s_m[w][q] - msafe);
+      const float f = __builtin_amdgcn_exp2f(s_m[w][q] - msafe);
       lsum += f * s_l[w][q];
       osum += f * s_o[w][q][d];
     }
-    const int64_t prow = (static_cast<int64_t>(b) * p.num_heads + qh0 + q) * p.max_splits + split;
-    p.part_o[prow * D + d] = lsum > 0.f ? osum / lsum : 0.f;
-    if (d == 0) p.part_lse[prow] = lsum > 0.f ? msafe + log2f(lsum) : -INFINITY;
+    const float o = lsum > 0.f ? osum / lsum : 0.f;
+    if (nsplits == 1) {
+      out[idx] = pack1(Tag{}, o);  // the only split: final output directly
+    } else {
+      const int64_t prow = prow0 + static_cast<int64_t>(q) * p.max_splits + split;
+      p.part_o[prow * D + d] = o;
+      if (d == 0) p.part_lse[prow] = lsum > 0.f ? msafe + log2f(lsum) : -INFINITY;
+    }
   }
 }
 
-// Pass 2: one wave per (query head, sequence).
+// Pass 2: one wave per (query head, sequence) merges the splits that
+// intersect [lo, L) with log-sum-exp weights.  Sequences with a single split
+// were finished by pass 1 and are skipped; empty sequences get zeros.
 template <class Tag, int D>
 __global__ __launch_bounds__(64) void paged_decode_merge(DecodeParams p) {
   constexpr int PER = D / 64;
@@ -416,34 +464,54 @@ __global__ __launch_bounds__(64) void paged_decode_merge(DecodeParams p) {
   const int lane = threadIdx.x;
   const int L = seq_len(p, b);
   uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + h) * D;
+  if (L == 0) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i) out[lane + 64 * i] = 0;
+    return;
+  }
+  const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
+  const int first = lo / p.split_tokens;
+  const int last = (L - 1) / p.split_tokens;
+  if (first == last) return;
+  const int64_t prow0 = (static_cast<int64_t>(b) * p.num_heads + h) * p.max_splits;
+  const float* lse = p.part_lse + prow0;
+  float M = -INFINITY;
+  for (int sp = first + lane; sp <= last; sp += 64) M = fmaxf(M, lse[sp]);
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
+  const float msafe = M == -INFINITY ? 0.f : M;
   float o[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) o[i] = 0.f;
-  if (L > 0) {
-    const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
-    const int first = lo / p.split_tokens;
-    const int last = (L - 1) / p.split_tokens;
-    const int64_t prow0 = (static_cast<int64_t>(b) * p.num_heads + h) * p.max_splits;
-    const float* lse = p.part_lse + prow0;
-    float M = -INFINITY;
-    for (int sp = first + lane; sp <= last; sp += 64) M = fmaxf(M, lse[sp]);
+  float wsum = 0.f;
+  // Splits in groups of 64: lane i owns the weight of split g + i, which every
+  // lane reads with a scalar readlane while several partial rows are in flight.
+  for (int g = first; g <= last; g += 64) {
+    const int n = min(64, last - g + 1);
+    const float wl = lane < n ? __builtin_amdgcn_exp2f(lse[g + lane] - msafe) : 0.f;
+    float ws = wl;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
-    const float msafe = M == -INFINITY ? 0.f : M;
-    float wsum = 0.f;
-    for (int sp = first; sp <= last; ++sp) {
-      const float w = exp2f(lse[sp] - msafe);
-      wsum += w;
-      const float* po = p.part_o + (prow0 + sp) * D;
+    for (int m = 32; m >= 1; m >>= 1) ws += __shfl_xor(ws, m);
+    wsum += ws;
+    const float* po = p.part_o + (prow0 + g) * D + lane;
+#pragma unroll 8
+    for (int i = 0; i < n; ++i) {
+      const float w =
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i));
 #pragma unroll
-      for (int i = 0; i < PER; ++i) o[i] = fmaf(w, po[lane + 64 * i], o[i]);
+      for (int k = 0; k < PER; ++k) o[k] = fmaf(w, po[static_cast<int64_t>(i) * D + 64 * k], o[k]);
     }
-    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-#pragma unroll
-    for (int i = 0; i < PER; ++i) o[i] *= inv;
   }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) out[lane + 64 * i] = pack1(Tag{}, o[i]);
+  for (int i = 0; i < PER; ++i) out[lane + 64 * i] = pack1(Tag{}, o[i] * inv);
+}
+
+// Zero output for a batch whose max_seqlen_k is 0 (no split workgroups run).
+__global__ __launch_bounds__(256) void zero_fill_u16(uint16_t* out, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * 256)
+    out[i] = 0;
 }
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -456,15 +524,28 @@ int64_t choose_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq
   return wgs512 >= 4096 ? 512 : 256;
 }
 
+dim3 split_grid(const DecodeParams& p) {
+#if OXIDE_GRID_MODE == 0
+  return dim3(p.max_splits, p.num_kv_heads, p.batch);
+#elif OXIDE_GRID_MODE == 1
+  return dim3(p.num_kv_heads, p.batch, p.max_splits);
+#else
+  const int64_t units = static_cast<int64_t>(p.batch) * p.max_splits;
+  return dim3(static_cast<unsigned>((units + kXcds - 1) / kXcds * kXcds * p.num_kv_heads));
+#endif
+}
+
 template <class Tag, int D, int G>
 void launch_split(const DecodeParams& p, int64_t batch, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(p.max_splits), static_cast<unsigned>(p.num_kv_heads),
-                  static_cast<unsigned>(batch));
+  const dim3 grid = split_grid(p);
   // split_tokens = kWaves * 16 * TILES.
-  if (p.split_tokens == 256)
-    hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 4>), grid, dim3(kThreads), 0, s, p);
-  else
-    hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 8>), grid, dim3(kThreads), 0, s, p);
+  switch (p.split_tokens) {
+    case 256: hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 4>), grid, dim3(kThreads), 0, s, p); break;
+#if OXIDE_SPLIT_TOKENS == 1024
+    case 1024: hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 16>), grid, dim3(kThreads), 0, s, p); break;
+#endif
+    default: hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 8>), grid, dim3(kThreads), 0, s, p); break;
+  }
 }
 
 template <class Tag, int D>
@@ -481,18 +562,40 @@ bool dispatch_group(const DecodeParams& p, int64_t batch, int group, hipStream_t
 
 template <class Tag>
 bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hipStream_t s) {
+  if (p.max_splits == 0) {
+    // max_seqlen_k == 0: every sequence is empty, the output is zeros.
+    const int64_t n = batch * p.num_heads * head_dim;
+    hipLaunchKernelGGL(zero_fill_u16, dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 4096))),
+                       dim3(256), 0, s, static_cast<uint16_t*>(p.out), n);
+    return true;
+  }
   const dim3 mgrid(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(batch));
   if (head_dim == 128) {
-    if (p.max_splits > 0 && !dispatch_group<Tag, 128>(p, batch, group, s)) return false;
+    if (!dispatch_group<Tag, 128>(p, batch, group, s)) return false;
     hipLaunchKernelGGL((paged_decode_merge<Tag, 128>), mgrid, dim3(64), 0, s, p);
     return true;
   }
   if (head_dim == 64) {
-    if (p.max_splits > 0 && !dispatch_group<Tag, 64>(p, batch, group, s)) return false;
+    if (!dispatch_group<Tag, 64>(p, batch, group, s)) return false;
     hipLaunchKernelGGL((paged_decode_merge<Tag, 64>), mgrid, dim3(64), 0, s, p);
     return true;
   }
   return false;
+}
+
+// Workspace: part_o [B, Hq, splits, D] f32 | part_lse [B, Hq, splits] f32,
+// each 256-byte aligned.
+struct WorkspaceLayout {
+  int64_t lse_off, total;
+};
+WorkspaceLayout workspace_layout(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                 int64_t head_dim, int64_t max_seqlen_k) {
+  const int64_t st = choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
+  const int64_t rows = batch * num_heads * ceil_div(max_seqlen_k, st);
+  WorkspaceLayout w;
+  w.lse_off = ceil_div(rows * head_dim * 4, 256) * 256;
+  w.total = w.lse_off + ceil_div(rows * 4, 256) * 256;
+  return w;
 }
 
 }  // namespace
@@ -507,11 +610,7 @@ extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t n
                                                         int64_t max_seqlen_k) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0)
     return 0;
-  const int64_t st = choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
-  const int64_t rows = batch * num_heads * ceil_div(max_seqlen_k, st);
-  // part_o (rows x D floats) then part_lse (rows floats), 256-byte aligned.
-  const int64_t o_bytes = ceil_div(rows * head_dim * 4, 256) * 256;
-  return static_cast<size_t>(o_bytes + ceil_div(rows * 4, 256) * 256);
+  return static_cast<size_t>(workspace_layout(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k).total);
 }
 
 extern "C" void paged_decode_attention(void* out, const void* q, const void* k_cache,
@@ -554,15 +653,14 @@ extern "C" void paged_decode_attention(void* out, const void* q, const void* k_c
   DecodeParams p{};
   const int64_t st = choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
   const int64_t max_splits = max_seqlen_k > 0 ? ceil_div(max_seqlen_k, st) : 0;
-  const int64_t rows = batch * num_heads * max_splits;
+  const WorkspaceLayout wl = workspace_layout(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k);
   p.q = q;
   p.k = k_cache;
   p.v = v_cache;
   p.cu_seqlens_k = cu_seqlens_k;
   p.block_table = block_table;
   p.part_o = static_cast<float*>(workspace);
-  p.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) +
-                                        ceil_div(rows * head_dim * 4, 256) * 256);
+  p.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.lse_off);
   p.out = out;
   p.max_blocks = max_blocks_per_seq;
   p.num_blocks = static_cast<int>(num_blocks);
@@ -573,6 +671,7 @@ extern "C" void paged_decode_attention(void* out, const void* q, const void* k_c
   p.window_left = window_left < 0 ? -1 : window_left;
   p.split_tokens = static_cast<int>(st);
   p.max_splits = static_cast<int>(max_splits);
+  p.batch = static_cast<int>(batch);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
   hipStream_t s = oxide::as_stream(stream);
   const bool ok = dtype == OXIDE_DTYPE_BF16
