@@ -10,8 +10,8 @@ N(0,1) data resident in HBM, steps rotating over distinct layers of the
 one left in the 256 MB MALL.
 
 Prints ONE JSON line.  value = algorithmic bytes of (append + attention) per
-step / wall time per step.  The dominant kernel pair (split-KV attention +
-merge) is also timed with HIP events on the stream it runs on -> roofline.
+step / wall time per step.  The attention call (split-KV kernel + LSE merge
+kernel) is also timed with HIP events on the stream it runs on -> roofline.
 cpu_baseline = the C oracle (test infrastructure, reference semantics) on a
 bounded sample of the same workload.
 """
@@ -200,7 +200,7 @@ def main() -> int:
         "tokens_per_s": round(cfg.batch / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "paged_decode_split (split-KV attention with fused merge)",
+                     "kernel": "paged_decode_split + paged_decode_merge (one attention call)",
                      "algorithmic_bytes": attn_bytes},
         **extra,
     }

@@ -64,7 +64,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 #define OXIDE_DECODE_OCCUPANCY
 #endif
 #ifndef OXIDE_GRID_MODE
-#define OXIDE_GRID_MODE 2  // workgroup -> (split, head, seq) order, see decode_work_item
+#define OXIDE_GRID_MODE 4  // workgroup -> (split, head, seq) order, see decode_work_item
 #endif
 #ifndef OXIDE_KV_NONTEMPORAL
 #define OXIDE_KV_NONTEMPORAL 1  // 1 = K/V streamed with non-temporal loads
@@ -192,6 +192,12 @@ __device__ __forceinline__ bool decode_work_item(const DecodeParams& p, int& spl
   if (u >= units) return false;
 #if OXIDE_GRID_MODE == 2
   b = u % p.batch; split = u / p.batch;
+#elif OXIDE_GRID_MODE == 4
+  // Split-major with the sequence rotated by the split index: unit u sits on
+  // XCD u % 8, so consecutive splits of one sequence land on different XCDs
+  // and ragged lengths spread evenly over the 8 L2s.
+  split = u / p.batch;
+  b = (u % p.batch + split) % p.batch;
 #else
   split = u % p.max_splits; b = u / p.max_splits;
 #endif
