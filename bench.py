@@ -30,6 +30,19 @@ sys.path.insert(0, str(REPO / "vllm-oxide_amd"))
 sys.path.insert(0, str(REPO))
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+# rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary of the same workload (calibrated HBM
+# bytes per attention call); the committed summary names the config it covers.
+TRAFFIC_PROFILE = {3: REPO / "profiles" / "paged_decode_cfg3.md"}
+
+
+def profiled_traffic(config: int):
+    path = TRAFFIC_PROFILE.get(config)
+    if path is None or not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_attention_call:"):
+            return int(line.split(":")[1])
+    return None
 
 
 def cpu_baseline(cfg, seed: int, threads: int, min_seconds: float = 10.0) -> dict:
@@ -199,7 +212,8 @@ def main() -> int:
         "append_gbps": round(app_gbps, 1),
         "tokens_per_s": round(cfg.batch / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": profiled_traffic(args.config),
                      "kernel": "paged_decode_split + paged_decode_merge (one attention call)",
                      "algorithmic_bytes": attn_bytes},
         **extra,

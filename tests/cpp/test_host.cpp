@@ -1,0 +1,372 @@
+// C++ tests of the host layer (vllm-oxide_amd/host), restating the reference's
+// own unit tests.  `test_host cpu` runs the host-logic tests (no GPU calls);
+// `test_host gpu` runs PagedKVCache / DecodeStep on device 0; `test_host hash
+// <seed> <hex bytes>` prints one XXH64 digest (the pytest driver compares it
+// with python-xxhash).
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "oxide_host.hpp"
+#include "paged_kv_cache.hpp"
+
+using namespace oxide::host;
+
+static int g_failures = 0;
+#define CHECK(cond)                                                          \
+  do {                                                                       \
+    if (!(cond)) {                                                           \
+      std::printf("FAIL %s:%d: %s\n", __FILE__, __LINE__, #cond);            \
+      ++g_failures;                                                          \
+    }                                                                        \
+  } while (0)
+
+template <class F>
+static bool throws(F f) {
+  try {
+    f();
+  } catch (const std::exception&) {
+    return true;
+  }
+  return false;
+}
+
+static std::vector<uint32_t> iota(uint32_t a, uint32_t b) {
+  std::vector<uint32_t> v;
+  for (uint32_t i = a; i < b; ++i) v.push_back(i);
+  return v;
+}
+
+// utils.rs:63-140
+static void test_layout() {
+  CHECK((kv_cache_layout_shape(28, 1024, 256, 4, 128) == std::array<std::size_t, 6>{2, 28, 1024, 256, 4, 128}));
+  CHECK((kv_cache_layout_shape(1, 2, 3, 4, 5) == std::array<std::size_t, 6>{2, 1, 2, 3, 4, 5}));
+  CHECK(round_up(0, 256) == 0 && round_up(256, 256) == 256 && round_up(1, 256) == 256);
+  CHECK(round_up(255, 256) == 256 && round_up(257, 256) == 512 && round_up(41, 1) == 41);
+  CHECK(round_up(4, 3) == 6 && round_up(7, 3) == 9 && round_up(3, 3) == 3);
+}
+
+// metadata.rs:82-218
+static void test_metadata() {
+  auto m = build_decode_metadata({5, 20, 3}, {{0}, {1, 2}, {3}}, {100, 200, 300});
+  CHECK((m.cu_seqlens_q == std::vector<uint32_t>{0, 1, 2, 3}));
+  CHECK((m.cu_seqlens_k == std::vector<uint32_t>{0, 5, 25, 28}));
+  CHECK(m.max_seqlen_q == 1 && m.max_seqlen_k == 20 && !m.is_prefill);
+  CHECK((m.slot_mapping == std::vector<int64_t>{100, 200, 300}));
+  CHECK(m.block_table.size() == 3 && m.block_table[1].size() == 2);
+  auto e = build_decode_metadata({}, {}, {});
+  CHECK(e.cu_seqlens_q == std::vector<uint32_t>{0} && e.cu_seqlens_k == std::vector<uint32_t>{0});
+  CHECK(e.max_seqlen_k == 0);
+  auto p = build_prefill_metadata({4, 8, 3}, {4, 16, 3}, {0, 0, 0});
+  CHECK((p.cu_seqlens_q == std::vector<uint32_t>{0, 4, 12, 15}));
+  CHECK((p.cu_seqlens_k == std::vector<uint32_t>{0, 4, 20, 23}));
+  CHECK(p.is_prefill && p.block_table.empty());
+  auto q = build_prefill_metadata({4, 12, 3}, {4, 20, 3}, {});
+  CHECK(q.max_seqlen_q == 12 && q.max_seqlen_k == 20);
+  // flash_attn.rs:74-86: pad with 0; empty table is an error.
+  auto t = pad_block_table({{7, 3}, {}, {1, 2, 9, 4}});
+  CHECK(t.rows == 3 && t.width == 4);
+  CHECK((t.data == std::vector<int32_t>{7, 3, 0, 0, 0, 0, 0, 0, 1, 2, 9, 4}));
+  CHECK(throws([] { pad_block_table({}); }));
+}
+
+// kv_cache_manager.rs:254-322
+static void test_slot_mapping() {
+  KvCacheManager mgr(10, 256);
+  Sequence s(iota(0, 10));
+  s.block_table = {42};
+  CHECK((mgr.compute_slot_mapping(s, 0, 3) == std::vector<int64_t>{42 * 256, 42 * 256 + 1, 42 * 256 + 2}));
+  Sequence s2(iota(0, 300));
+  s2.block_table = {10, 20};
+  CHECK((mgr.compute_slot_mapping(s2, 254, 4) ==
+         std::vector<int64_t>{10 * 256 + 254, 10 * 256 + 255, 20 * 256, 20 * 256 + 1}));
+  Sequence s3(iota(0, 3 * 256 + 50));
+  s3.block_table = {5, 6, 7, 8};
+  auto full = mgr.compute_slot_mapping(s3, 0, 3 * 256 + 50);
+  bool ok = full.size() == 3 * 256 + 50;
+  for (std::size_t i = 0; ok && i < full.size(); ++i)
+    ok = full[i] == static_cast<int64_t>(s3.block_table[i / 256] * 256 + i % 256);
+  CHECK(ok);
+  CHECK(mgr.compute_slot_mapping(Sequence({1, 2, 3}), 0, 0).empty());
+  Sequence s4(iota(0, 10));
+  s4.block_table = {1};
+  CHECK(mgr.compute_slot_mapping(s4, 256, 1) == std::vector<int64_t>{-1});
+}
+
+// block_pool.rs:371-885
+static void test_block_pool() {
+  // compute_hash properties
+  CHECK(BlockPool::compute_hash({1, 2, 3}, -1) != BlockPool::compute_hash({1, 2, 3}, 0));
+  CHECK(BlockPool::compute_hash({1, 2, 3}, 0) != BlockPool::compute_hash({1, 2, 3}, 42));
+  CHECK(BlockPool::compute_hash({10, 20, 30, 40}, 100) == BlockPool::compute_hash({10, 20, 30, 40}, 100));
+  CHECK(BlockPool::compute_hash({1, 2, 3}, -1) != BlockPool::compute_hash({3, 2, 1}, -1));
+  {  // prefix -1 omits the prefix bytes; prefix 0 prepends 8 zero bytes
+    const uint8_t b78[8] = {7, 0, 0, 0, 8, 0, 0, 0};
+    CHECK(BlockPool::compute_hash({7, 8}, -1) == static_cast<int64_t>(xxh64(b78, 8, 0)));
+    uint8_t z[16] = {0};
+    std::memcpy(z + 8, b78, 8);
+    CHECK(BlockPool::compute_hash({7, 8}, 0) == static_cast<int64_t>(xxh64(z, 16, 0)));
+  }
+  {  // can_allocate
+    BlockPool pool(10, 256);
+    CHECK(pool.can_allocate(Sequence({})) == std::optional<std::size_t>(0));
+    BlockPool small(2, 256);
+    CHECK(!small.can_allocate(Sequence(iota(0, 4 * 256 + 1))).has_value());
+    CHECK(small.can_allocate(Sequence(iota(0, 2 * 256))) == std::optional<std::size_t>(0));
+  }
+  {  // counts cached blocks
+    BlockPool pool(10, 256);
+    auto t1 = iota(0, 256), t2 = iota(256, 512);
+    const int64_t h1 = BlockPool::compute_hash(t1, -1), h2 = BlockPool::compute_hash(t2, h1);
+    const std::size_t b1 = pool.allocate_block(), b2 = pool.allocate_block();
+    pool.register_hash(b1, h1, t1);
+    pool.register_hash(b2, h2, t2);
+    CHECK(pool.can_allocate(Sequence(iota(0, 3 * 256))) == std::optional<std::size_t>(2));
+  }
+  {  // allocate sets table and cached tokens; double allocate errors
+    BlockPool pool(10, 256);
+    Sequence s(iota(0, 3 * 256 + 50));
+    CHECK(pool.can_allocate(s) == std::optional<std::size_t>(0));
+    pool.allocate(s, 0);
+    CHECK(s.block_table.size() == 4 && s.num_cached_tokens == 0);
+    CHECK(throws([&] { pool.allocate(s, 0); }));
+  }
+  {  // shared prefix: ref counts, release only at zero
+    BlockPool pool(10, 256);
+    auto prefix = iota(0, 256);
+    const int64_t h = BlockPool::compute_hash(prefix, -1);
+    Sequence a(prefix);
+    pool.allocate(a, 0);
+    const std::size_t id = a.block_table[0];
+    pool.register_hash(id, h, prefix);
+    auto tb = prefix;
+    tb.push_back(999);
+    Sequence b(tb);
+    const auto nc = pool.can_allocate(b);
+    CHECK(nc == std::optional<std::size_t>(1));
+    pool.allocate(b, *nc);
+    CHECK(pool.block(id).ref_count == 2 && b.block_table[0] == id && b.block_table[1] != id);
+    CHECK(b.num_cached_tokens == 256);
+    pool.deallocate(a);
+    CHECK(pool.block(id).ref_count == 1 && pool.is_used(id));
+    pool.deallocate(b);
+    CHECK(pool.block(id).ref_count == 0 && !pool.is_used(id));
+    CHECK(pool.block(id).token_ids == prefix);  // the original block's tokens are untouched
+    // The freed, still-hashed block is found again and moved back from the free list.
+    Sequence c(tb);
+    CHECK(pool.can_allocate(c) == std::optional<std::size_t>(1));
+    pool.allocate(c, 1);
+    CHECK(c.block_table[0] == id && pool.block(id).ref_count == 1);
+  }
+  {  // deallocate releases; twice is a no-op
+    BlockPool pool(5, 256);
+    Sequence s(iota(0, 2 * 256 + 1));
+    pool.allocate(s, 0);
+    CHECK(pool.num_free_blocks() == 2);
+    pool.deallocate(s);
+    CHECK(pool.num_free_blocks() == 5 && s.block_table.empty() && s.num_cached_tokens == 0);
+    pool.deallocate(s);
+    CHECK(s.block_table.empty());
+  }
+  {  // can_append / may_append: a new block iff num_tokens % 256 == 1
+    BlockPool pool(1, 256);
+    Sequence s(iota(0, 256));
+    pool.allocate(s, 0);
+    CHECK(pool.num_free_blocks() == 0 && pool.can_append(s));
+    s.append_token(7);  // 257 tokens: the next token opens block 1
+    CHECK(!pool.can_append(s));
+    CHECK(throws([&] { pool.may_append(s); }));
+    BlockPool pool2(2, 256);
+    Sequence t(iota(0, 256));
+    pool2.allocate(t, 0);
+    t.append_token(7);
+    pool2.may_append(t);
+    CHECK(t.block_table.size() == 2 && pool2.num_free_blocks() == 0);
+    t.append_token(8);  // 258: no new block
+    pool2.may_append(t);
+    CHECK(t.block_table.size() == 2);
+  }
+  {  // hash_blocks: incremental chain equals one pass
+    BlockPool p1(10, 256), p2(10, 256);
+    Sequence a(iota(0, 3 * 256)), b(iota(0, 3 * 256));
+    p1.allocate(a, 0);
+    p2.allocate(b, 0);
+    a.num_cached_tokens = 0;
+    a.num_scheduled_tokens = 3 * 256;
+    p1.hash_blocks(a);
+    b.num_cached_tokens = 0;
+    b.num_scheduled_tokens = 256;
+    p2.hash_blocks(b);
+    b.num_cached_tokens = 256;
+    b.num_scheduled_tokens = 2 * 256;
+    p2.hash_blocks(b);
+    for (int i = 0; i < 3; ++i) {
+      CHECK(p1.block(a.block_table[i]).hash != -1);
+      CHECK(p1.block(a.block_table[i]).hash == p2.block(b.block_table[i]).hash);
+    }
+    int64_t h = -1;
+    for (int i = 0; i < 3; ++i) h = BlockPool::compute_hash(a.block(i), h);
+    CHECK(p1.block(a.block_table[2]).hash == h);
+  }
+  {  // FIFO free list: freed blocks go to the back
+    BlockPool pool(3, 256);
+    const std::size_t x = pool.allocate_block();
+    CHECK(x == 0);
+    Sequence s(iota(0, 10));
+    s.block_table = {x};
+    pool.deallocate(s);
+    CHECK(pool.allocate_block() == 1 && pool.allocate_block() == 2 && pool.allocate_block() == 0);
+  }
+}
+
+// ------------------------------------------------------------------- GPU
+static uint16_t f2bf(float f) {
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+static float bf2f(uint16_t h) {
+  const uint32_t u = static_cast<uint32_t>(h) << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// attention/mod.rs:161-230 reshape_and_cache_writes_correct_slots, through PagedKVCache.
+static void test_gpu_append_known_answer() {
+  const std::size_t H = 2, D = 64, T = 3;
+  PagedKVCache cache(1, 4, 256, H, D, OXIDE_DTYPE_BF16);
+  CHECK((cache.buffer_shape() == std::array<std::size_t, 6>{2, 1, 4, 256, 2, 64}));
+  std::vector<uint16_t> key(T * H * D), val(T * H * D);
+  for (std::size_t i = 0; i < key.size(); ++i) {
+    key[i] = f2bf(static_cast<float>(i));
+    val[i] = f2bf(1000.f + static_cast<float>(i));
+  }
+  const std::vector<int64_t> slots = {0, 256, 512};
+  void *dk, *dv, *ds;
+  (void)hipMalloc(&dk, key.size() * 2);
+  (void)hipMalloc(&dv, val.size() * 2);
+  (void)hipMalloc(&ds, 3 * 8);
+  (void)hipMemcpy(dk, key.data(), key.size() * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(dv, val.data(), val.size() * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(ds, slots.data(), 3 * 8, hipMemcpyHostToDevice);
+  cache.reshape_and_cache(0, dk, dv, static_cast<const int64_t*>(ds), T, nullptr);
+  const std::size_t view = 4 * 256 * H * D;
+  std::vector<uint16_t> kc(view), vc(view);
+  (void)hipMemcpy(kc.data(), cache.k_cache(0), view * 2, hipMemcpyDeviceToHost);
+  (void)hipMemcpy(vc.data(), cache.v_cache(0), view * 2, hipMemcpyDeviceToHost);
+  const std::size_t row = H * D;
+  // k[0,0] == key[0], k[1,0] == key[1], v[2,0] == value[2], max diff 0.
+  CHECK(std::memcmp(kc.data() + 0 * 256 * row, key.data() + 0 * row, row * 2) == 0);
+  CHECK(std::memcmp(kc.data() + 1 * 256 * row, key.data() + 1 * row, row * 2) == 0);
+  CHECK(std::memcmp(vc.data() + 2 * 256 * row, val.data() + 2 * row, row * 2) == 0);
+  std::size_t nonzero = 0;
+  for (uint16_t x : kc) nonzero += x != 0;
+  std::size_t want = 0;
+  for (uint16_t x : key) want += x != 0;
+  CHECK(nonzero == want);
+  (void)hipFree(dk);
+  (void)hipFree(dv);
+  (void)hipFree(ds);
+}
+
+// attention/mod.rs:277-323 flash_attn_decode_runs (ctx 32, 4 heads, 4 kv heads,
+// D 64): through DecodeStep, checked against an in-test fp64 softmax.
+static void test_gpu_decode_step() {
+  const std::size_t Hq = 4, H = 4, D = 64, ctx = 32;
+  PagedKVCache cache(2, 1, 256, H, D, OXIDE_DTYPE_BF16);
+  DecodeStep step(cache, Hq);
+  // Fill keys 0..30 through appends of a 31-token "prefill", then decode token 31.
+  uint64_t s = 12345;
+  auto rnd = [&s]() {
+    s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+    return static_cast<float>(static_cast<int64_t>(s >> 11) % 2000 - 1000) / 1000.f;
+  };
+  std::vector<uint16_t> k(ctx * H * D), v(ctx * H * D), q(Hq * D);
+  for (auto& x : k) x = f2bf(rnd());
+  for (auto& x : v) x = f2bf(rnd());
+  for (auto& x : q) x = f2bf(rnd());
+  std::vector<int64_t> prefill_slots;
+  for (std::size_t i = 0; i + 1 < ctx; ++i) prefill_slots.push_back(static_cast<int64_t>(i));
+  void *dk, *dv, *dq, *dout, *ds;
+  (void)hipMalloc(&dk, k.size() * 2);
+  (void)hipMalloc(&dv, v.size() * 2);
+  (void)hipMalloc(&dq, q.size() * 2);
+  (void)hipMalloc(&dout, q.size() * 2);
+  (void)hipMalloc(&ds, prefill_slots.size() * 8);
+  (void)hipMemcpy(dk, k.data(), k.size() * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(dv, v.data(), v.size() * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(dq, q.data(), q.size() * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(ds, prefill_slots.data(), prefill_slots.size() * 8, hipMemcpyHostToDevice);
+  for (std::size_t layer = 0; layer < 2; ++layer)
+    cache.reshape_and_cache(layer, dk, dv, static_cast<const int64_t*>(ds), ctx - 1, nullptr);
+  // Decode step: the new token (row 31 of k/v) goes to slot 31, then attention over 32 keys.
+  KvCacheManager mgr(1, 256);
+  Sequence seq(iota(0, ctx));
+  seq.block_table = {0};
+  const auto slot = mgr.compute_slot_mapping(seq, ctx - 1, 1);
+  CHECK(slot == std::vector<int64_t>{31});
+  step.upload(build_decode_metadata({static_cast<uint32_t>(ctx)}, {{0}}, slot), nullptr);
+  const float scale = 1.f / std::sqrt(static_cast<float>(D));
+  const char* knew = static_cast<const char*>(dk) + (ctx - 1) * H * D * 2;
+  const char* vnew = static_cast<const char*>(dv) + (ctx - 1) * H * D * 2;
+  for (std::size_t layer = 0; layer < 2; ++layer) {
+    step.run_layer(layer, dq, knew, vnew, dout, scale, -1, nullptr);
+    std::vector<uint16_t> out(q.size());
+    (void)hipMemcpy(out.data(), dout, out.size() * 2, hipMemcpyDeviceToHost);
+    double max_err = 0;
+    for (std::size_t h = 0; h < Hq; ++h) {
+      const std::size_t kh = h / (Hq / H);
+      std::vector<double> sc(ctx);
+      double mx = -1e300;
+      for (std::size_t j = 0; j < ctx; ++j) {
+        double dot = 0;
+        for (std::size_t d = 0; d < D; ++d)
+          dot += static_cast<double>(bf2f(q[h * D + d])) * bf2f(k[(j * H + kh) * D + d]);
+        sc[j] = dot * scale;
+        mx = std::max(mx, sc[j]);
+      }
+      double l = 0;
+      for (auto& x : sc) l += (x = std::exp(x - mx));
+      for (std::size_t d = 0; d < D; ++d) {
+        double o = 0;
+        for (std::size_t j = 0; j < ctx; ++j) o += sc[j] / l * bf2f(v[(j * H + kh) * D + d]);
+        const double got = bf2f(out[h * D + d]);
+        CHECK(!std::isnan(got));
+        max_err = std::max(max_err, std::fabs(got - o));
+      }
+    }
+    CHECK(max_err <= 2e-2);
+  }
+  for (void* p : {dk, dv, dq, dout, ds}) (void)hipFree(p);
+}
+
+int main(int argc, char** argv) {
+  const std::string mode = argc > 1 ? argv[1] : "cpu";
+  if (mode == "hash" && argc == 4) {
+    const std::string hex = argv[3];
+    std::vector<uint8_t> bytes;
+    for (std::size_t i = 0; i + 1 < hex.size(); i += 2)
+      bytes.push_back(static_cast<uint8_t>(std::strtoul(hex.substr(i, 2).c_str(), nullptr, 16)));
+    std::printf("%llu\n", static_cast<unsigned long long>(
+                              xxh64(bytes.data(), bytes.size(), std::strtoull(argv[2], nullptr, 10))));
+    return 0;
+  }
+  if (mode == "cpu") {
+    test_layout();
+    test_metadata();
+    test_slot_mapping();
+    test_block_pool();
+  } else if (mode == "gpu") {
+    test_gpu_append_known_answer();
+    test_gpu_decode_step();
+  } else {
+    std::printf("usage: test_host cpu|gpu|hash <seed> <hex>\n");
+    return 2;
+  }
+  std::printf("%s: %d failures\n", mode.c_str(), g_failures);
+  return g_failures == 0 ? 0 : 1;
+}

@@ -21,6 +21,8 @@ HOST = PKG / "host"
 INCLUDE = REPO / "include"
 BUILD = PKG / "_build"
 LIB = PKG / "liboxide_paged_kv.so"
+HOST_TEST_SRC = REPO / "tests" / "cpp" / "test_host.cpp"
+HOST_TEST_BIN = REPO / "tests" / "cpp" / "build" / "test_host"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -58,9 +60,22 @@ def build(verbose: bool = False) -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    build_host_test()
     if verbose:
         print(f"built {LIB}")
     return LIB
+
+
+def build_host_test() -> Path:
+    """C++ test binary of the host layer (tests/cpp/test_host.cpp), linked to the library."""
+    HOST_TEST_BIN.parent.mkdir(parents=True, exist_ok=True)
+    cmd = [HIPCC, *HIP_FLAGS, "-I", str(INCLUDE), "-I", str(HOST), str(HOST_TEST_SRC), "-o",
+           str(HOST_TEST_BIN), "-L", str(PKG), "-loxide_paged_kv", f"-Wl,-rpath,{PKG}",
+           "-Wl,-rpath,$ORIGIN/../../../vllm-oxide_amd"]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"hipcc failed for {HOST_TEST_SRC.name}:\n{r.stdout}\n{r.stderr}")
+    return HOST_TEST_BIN
 
 
 if __name__ == "__main__":

@@ -1,0 +1,139 @@
+// PagedKVCache and DecodeStep over the C ABI (see paged_kv_cache.hpp).
+#include "paged_kv_cache.hpp"
+
+#include <algorithm>
+
+namespace oxide::host {
+
+namespace {
+void check(hipError_t e, const char* what) {
+  if (e != hipSuccess) throw HipError(std::string(what) + ": " + hipGetErrorString(e));
+}
+void check_lib(const char* what) {
+  const int code = oxide_last_error();
+  if (code != OXIDE_OK) {
+    oxide_clear_error();
+    throw HipError(std::string(what) + ": " + oxide_error_string(code));
+  }
+}
+}  // namespace
+
+PagedKVCache::PagedKVCache(std::size_t num_layers, std::size_t num_blocks, std::size_t block_size,
+                           std::size_t num_kv_heads, std::size_t head_dim, int dtype)
+    : num_layers_(num_layers),
+      num_blocks_(num_blocks),
+      block_size_(block_size),
+      num_kv_heads_(num_kv_heads),
+      head_dim_(head_dim),
+      dtype_(dtype) {
+  if (elem_bytes() == 0) throw std::invalid_argument("unsupported KV cache dtype");
+  const auto s = buffer_shape();
+  std::size_t bytes = elem_bytes();
+  for (std::size_t d : s) bytes *= d;
+  check(hipMalloc(&buffer_, std::max<std::size_t>(bytes, 1)), "hipMalloc(PagedKVCache)");
+  check(hipMemset(buffer_, 0, bytes), "hipMemset(PagedKVCache)");  // Tensor::zeros, mod.rs:68
+}
+
+PagedKVCache::~PagedKVCache() {
+  if (buffer_) (void)hipFree(buffer_);
+}
+
+std::size_t PagedKVCache::elem_bytes() const {
+  return dtype_ == OXIDE_DTYPE_F32 ? 4 : (dtype_ == OXIDE_DTYPE_F16 || dtype_ == OXIDE_DTYPE_BF16 ? 2 : 0);
+}
+
+std::array<std::size_t, 6> PagedKVCache::buffer_shape() const {
+  return kv_cache_layout_shape(num_layers_, num_blocks_, block_size_, num_kv_heads_, head_dim_);
+}
+
+void* PagedKVCache::k_cache(std::size_t layer) const {
+  if (layer >= num_layers_) throw std::out_of_range("layer");
+  const std::size_t view = num_blocks_ * block_size_ * num_kv_heads_ * head_dim_ * elem_bytes();
+  return static_cast<char*>(buffer_) + layer * view;
+}
+
+void* PagedKVCache::v_cache(std::size_t layer) const {
+  if (layer >= num_layers_) throw std::out_of_range("layer");
+  const std::size_t view = num_blocks_ * block_size_ * num_kv_heads_ * head_dim_ * elem_bytes();
+  return static_cast<char*>(buffer_) + (num_layers_ + layer) * view;
+}
+
+void PagedKVCache::reshape_and_cache(std::size_t layer, const void* key, const void* value,
+                                     const int64_t* slot_mapping, std::size_t num_tokens,
+                                     hipStream_t stream) const {
+  ::reshape_and_cache(key, value, k_cache(layer), v_cache(layer), slot_mapping,
+                      static_cast<int64_t>(num_tokens), static_cast<int64_t>(num_kv_heads_),
+                      static_cast<int64_t>(head_dim_), dtype_, stream);
+  check_lib("reshape_and_cache");
+}
+
+void PagedKVCache::copy_blocks(std::size_t layer, const int64_t* block_mapping,
+                               std::size_t num_pairs, hipStream_t stream) const {
+  ::copy_blocks(k_cache(layer), v_cache(layer), block_mapping, static_cast<int64_t>(num_pairs),
+                static_cast<int64_t>(block_size_ * num_kv_heads_ * head_dim_), dtype_, stream);
+  check_lib("copy_blocks");
+}
+
+DecodeStep::DecodeStep(const PagedKVCache& cache, std::size_t num_heads)
+    : cache_(cache), num_heads_(num_heads) {}
+
+DecodeStep::~DecodeStep() {
+  for (void* p : {d_cu_, d_table_, d_slots_, d_ws_})
+    if (p) (void)hipFree(p);
+}
+
+void DecodeStep::ensure(void** ptr, std::size_t* cap, std::size_t bytes) {
+  if (bytes <= *cap) return;
+  if (*ptr) check(hipFree(*ptr), "hipFree");
+  *ptr = nullptr;
+  check(hipMalloc(ptr, bytes), "hipMalloc(DecodeStep)");
+  *cap = bytes;
+}
+
+void DecodeStep::upload(const AttnMetadata& meta, hipStream_t stream) {
+  if (meta.is_prefill) throw std::invalid_argument("DecodeStep needs decode metadata");
+  batch_ = meta.cu_seqlens_k.empty() ? 0 : meta.cu_seqlens_k.size() - 1;
+  if (batch_ == 0) return;
+  const PaddedTable t = pad_block_table(meta.block_table);
+  max_blocks_ = t.width;
+  max_seqlen_k_ = meta.max_seqlen_k;
+  // Synchronise before overwriting the staging copies a previous async upload may still read.
+  check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  h_cu_ = meta.cu_seqlens_k;
+  h_table_ = t.data;
+  h_slots_ = meta.slot_mapping;
+  ensure(&d_cu_, &cap_cu_, h_cu_.size() * sizeof(uint32_t));
+  ensure(&d_table_, &cap_table_, std::max<std::size_t>(h_table_.size(), 1) * sizeof(int32_t));
+  ensure(&d_slots_, &cap_slots_, std::max<std::size_t>(h_slots_.size(), 1) * sizeof(int64_t));
+  check(hipMemcpyAsync(d_cu_, h_cu_.data(), h_cu_.size() * sizeof(uint32_t), hipMemcpyHostToDevice,
+                       stream), "upload cu_seqlens_k");
+  check(hipMemcpyAsync(d_table_, h_table_.data(), h_table_.size() * sizeof(int32_t),
+                       hipMemcpyHostToDevice, stream), "upload block_table");
+  check(hipMemcpyAsync(d_slots_, h_slots_.data(), h_slots_.size() * sizeof(int64_t),
+                       hipMemcpyHostToDevice, stream), "upload slot_mapping");
+  const std::size_t ws = paged_decode_attention_workspace_size(
+      static_cast<int64_t>(batch_), static_cast<int64_t>(num_heads_),
+      static_cast<int64_t>(cache_.num_kv_heads()), static_cast<int64_t>(cache_.head_dim()),
+      static_cast<int64_t>(max_seqlen_k_));
+  ensure(&d_ws_, &cap_ws_, std::max<std::size_t>(ws, 1));
+}
+
+void DecodeStep::run_layer(std::size_t layer, const void* q, const void* key, const void* value,
+                           void* out, float softmax_scale, int32_t window_left,
+                           hipStream_t stream) {
+  if (batch_ == 0) return;
+  cache_.reshape_and_cache(layer, key, value, static_cast<const int64_t*>(d_slots_),
+                           h_slots_.size(), stream);
+  ::paged_decode_attention(out, q, cache_.k_cache(layer), cache_.v_cache(layer),
+                           static_cast<const uint32_t*>(d_cu_), static_cast<const int32_t*>(d_table_),
+                           static_cast<int64_t>(max_blocks_), static_cast<int64_t>(cache_.num_blocks()),
+                           static_cast<int64_t>(batch_), static_cast<int64_t>(num_heads_),
+                           static_cast<int64_t>(cache_.num_kv_heads()),
+                           static_cast<int64_t>(cache_.head_dim()),
+                           static_cast<int64_t>(cache_.block_size()),
+                           static_cast<int64_t>(max_seqlen_k_), window_left, softmax_scale, d_ws_,
+                           cap_ws_, cache_.dtype(), stream);
+  check_lib("paged_decode_attention");
+}
+
+}  // namespace oxide::host
