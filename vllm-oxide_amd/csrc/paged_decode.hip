@@ -11,28 +11,23 @@
 // view [num_blocks, BS, Hkv, D].  Accumulation is fp32; the output is rounded
 // to the cache dtype once.
 //
-// Pass 1 (paged_decode_split): one workgroup per (split, kv head, sequence).
-// A split is split_tokens consecutive logical keys; its 4 waves take a quarter
-// each.  A wave walks its keys in batches of NT tiles of 16 keys:
-//   * K rows: lane (r16 = lane % 16, grp = lane / 16) loads 16 bytes at
-//     d = 8*(grp + 4*kk) of key r16, kk < D/32: per instruction 16 rows x 64
-//     contiguous bytes, the whole 256-byte row over D/32 instructions.
-//   * QK^T on the matrix cores: v_mfma_f32_16x16x32_{bf16,f16} with
-//     A = the G query rows of this kv head, replicated to fill the 16 MFMA
-//     rows (row r holds query r % G), B = K^T (16 keys).  With the k index of
-//     step kk taken as d = 8*(grp + 4*kk) + i in both operands, the dot
-//     products come out in the C layout lane l -> rows 4*(l/16)+j, col l%16,
-//     i.e. every lane holds the scores of key r16 for queries (4*grp+j) % G.
-//     Replication means no lane needs a shuffle to find its key's scores.
-//   * online softmax in the log2 domain (scale folded with log2 e), maxima
-//     reduced over the 16 keys of a row with DPP, probabilities written to a
-//     per-wave LDS strip [tile][key][G].
-//   * PV on the VALU: V rows are loaded chunk-fixed (lane % (D/8) picks a
-//     16-byte d chunk, lane / (D/8) picks the row), so each lane accumulates
-//     8 d values for all G queries (8*G fp32 registers) and reads the G
-//     probabilities of its row with one LDS broadcast read per row.
-//   Waves are then merged through LDS and the split writes its normalised
-//   partial output o (fp32, [B, Hq, max_splits, D]) and log2-sum-exp.
+// Pass 1 (paged_decode_split): one workgroup of 4 waves per (split, kv head,
+// sequence); a split is 512 consecutive logical keys (256 for small batches),
+// 128 per wave, walked as 16-key tiles in straight-line code with a register
+// double buffer (tile t+1's loads are in flight while tile t computes; loads
+// past the wave's last key are clamped to a fetched tile and masked).
+//   * K and V rows are loaded as whole 256-byte head rows per 16 lanes, four
+//     rows per instruction, with non-temporal hints: the shape that streams at
+//     full HBM rate.  K is transposed through a wave-private LDS tile into the
+//     MFMA layout; V rows are staged in LDS for the transposing reads.
+//   * S^T = K . Q^T and O += P . V both on the matrix cores
+//     (v_mfma_f32_16x16x32_{bf16,f16}); the tile math is described above
+//     paged_decode_split below.
+//   * online softmax per query in the log2 domain (scale folded with log2 e).
+//   The 4 waves are merged through LDS; a sequence with a single split writes
+//   its output directly, otherwise the split writes its normalised partial
+//   output o (fp32, [B, Hq, max_splits, D]) and log2-sum-exp.
+// Workgroup order is XCD-aware (decode_work_item).
 // Pass 2 (paged_decode_merge): one wave per (query head, sequence) merges the
 // splits that intersect [lo, L) with log-sum-exp weights and writes out.
 //
@@ -48,7 +43,6 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // Build-time tuning knobs (defaults are the tuned values).
@@ -92,17 +86,6 @@ __device__ __forceinline__ floatx4 mfma16x16x32(F16Tag, uint4 a, uint4 b, floatx
                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
-// Two packed 16-bit values -> fp32 (exact for both formats).
-__device__ __forceinline__ void unpack2(Bf16Tag, uint32_t w, float& lo, float& hi) {
-  lo = __uint_as_float(w << 16);
-  hi = __uint_as_float(w & 0xffff0000u);
-}
-__device__ __forceinline__ void unpack2(F16Tag, uint32_t w, float& lo, float& hi) {
-  const f16x2_t h = __builtin_bit_cast(f16x2_t, w);
-  lo = static_cast<float>(h.x);
-  hi = static_cast<float>(h.y);
-}
-
 // fp32 -> 16-bit storage, round to nearest even.
 __device__ __forceinline__ uint16_t pack1(Bf16Tag, float f) {
   const uint32_t u = __float_as_uint(f);
@@ -111,28 +94,6 @@ __device__ __forceinline__ uint16_t pack1(Bf16Tag, float f) {
 }
 __device__ __forceinline__ uint16_t pack1(F16Tag, float f) {
   return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
-}
-
-// Reductions over the 16 lanes of a DPP row (lanes 16r .. 16r+15).
-// quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror.
-template <int kCtrl>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(
-      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), kCtrl, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float row16_max(float x) {
-  x = fmaxf(x, dpp<0xB1>(x));
-  x = fmaxf(x, dpp<0x4E>(x));
-  x = fmaxf(x, dpp<0x141>(x));
-  x = fmaxf(x, dpp<0x140>(x));
-  return x;
-}
-__device__ __forceinline__ float row16_sum(float x) {
-  x += dpp<0xB1>(x);
-  x += dpp<0x4E>(x);
-  x += dpp<0x141>(x);
-  x += dpp<0x140>(x);
-  return x;
 }
 
 struct DecodeParams {
@@ -205,31 +166,63 @@ __device__ __forceinline__ bool decode_work_item(const DecodeParams& p, int& spl
 #endif
 }
 
+// ---------------------------------------------------------------------------
+// Pass 1 tile math:
+//   * S^T = K . Q^T: A = the K tile from LDS (row = key r16), B = the query
+//     rows (column = query slot r16, slot s holds query s % G).  Lane l then
+//     holds the scores of keys 4*(l/16)+j (j < 4) for query slot l % 16.
+//   * softmax per query slot: maxima over the lane's 4 keys, then across the
+//     4 lane groups (xor 16, 32).
+//   * two 16-key tiles make one 32-key PV step on the matrix cores,
+//     O[slot][d] += P[slot][k] V[k][d]: the lane's own probabilities of the two
+//     tiles are exactly its A operand (k slots 0-3 = keys 4g..4g+3 of the even
+//     tile, 4-7 = the same keys of the odd tile), and the B operand is read
+//     from a row-major V tile in LDS with ds_read_b64_tr_b16, which hands lane
+//     i of each 16-lane group element (i % 4) of lane 4j + i/4's 8-byte read:
+//     reading V[4g + i/4][d0 + 4*(i%4)] gives lane i V[4g + j][d0 + i].
+//   * 32 fp32 accumulators per lane for D = 128, whatever the group size.
+// V rows in LDS are padded to D*2 + 32 bytes so the 4 rows one 16-lane group
+// reads land on disjoint banks.
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16_t*)((__attribute__((address_space(3))) char*)(p)));
+  return __builtin_bit_cast(uint2, r);
+}
+
+// Two fp32 probabilities -> packed 16-bit pair of the MFMA input type.
+__device__ __forceinline__ uint32_t pack2(Bf16Tag, float lo, float hi) {
+  return static_cast<uint32_t>(pack1(Bf16Tag{}, lo)) | (static_cast<uint32_t>(pack1(Bf16Tag{}, hi)) << 16);
+}
+__device__ __forceinline__ uint32_t pack2(F16Tag, float lo, float hi) {
+  return static_cast<uint32_t>(pack1(F16Tag{}, lo)) | (static_cast<uint32_t>(pack1(F16Tag{}, hi)) << 16);
+}
+
 template <class Tag, int D, int G, int TILES>
 __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_split(DecodeParams p) {
-  constexpr int KK = D / 32;     // MFMA k-steps per key row
-  constexpr int CH = D / 8;      // 16-byte chunks per row
-  constexpr int RPL = 64 / CH;   // rows per wave-wide K/V load
-  constexpr int VL = 16 / RPL;   // K (and V) loads per 16-key tile
-  constexpr int GP = G < 4 ? 4 : G;  // padded LDS row (floats) for 16-byte reads
-  constexpr int WT = 16 * TILES;     // keys per wave; split = kWaves * WT
-
-  // K tile in MFMA order: row r holds 16-byte chunk c at slot c ^ (r % CH),
-  // which keeps both the row-wise writes and the column-wise MFMA reads
-  // spread over all LDS banks.
-  __shared__ __align__(16) uint4 s_k[kWaves][16][CH];
-  __shared__ __align__(16) float s_p[kWaves][16][GP];
-  __shared__ __align__(16) float s_alpha[kWaves][GP];
-  __shared__ __align__(16) float s_o[kWaves][G][D];
-  __shared__ float s_m[kWaves][G];
-  __shared__ float s_l[kWaves][G];
+  static_assert(TILES % 2 == 0, "PV steps take two 16-key tiles");
+  constexpr int KK = D / 32;
+  constexpr int CH = D / 8;
+  constexpr int RPL = 64 / CH;
+  constexpr int VL = 16 / RPL;
+  constexpr int NDT = D / 16;          // 16-column output tiles
+  constexpr int VRS = 2 * D + 32;      // padded V row in LDS (bytes)
+  constexpr int WT = 16 * TILES;
+  constexpr int KBYTES = 16 * CH * 16;                  // one K tile
+  constexpr int WAVE_BYTES = KBYTES + 32 * VRS;         // K tile + 32 V rows
+  constexpr int LOOP_BYTES = kWaves * WAVE_BYTES;
+  constexpr int EPI_BYTES = kWaves * G * D * 4 + 2 * kWaves * G * 4;
+  constexpr int SMEM = LOOP_BYTES > EPI_BYTES ? LOOP_BYTES : EPI_BYTES;
+  __shared__ __align__(16) char smem[SMEM];
 
   int split, kh, b;
   if (!decode_work_item(p, split, kh, b)) return;
   const int L = seq_len(p, b);
   const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
   const int s0 = split * (kWaves * WT);
-  if (s0 >= L || s0 + kWaves * WT <= lo) return;  // not one of this sequence's splits
+  if (s0 >= L || s0 + kWaves * WT <= lo) return;
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -237,58 +230,40 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
   const int grp = lane >> 4;
   const int vch = lane % CH;
   const int vrow = lane / CH;
-  // This wave's keys: [a, e) inside its region [w0, w0 + WT).  Wave-uniform.
   const int w0 = s0 + wave * WT;
   const int a = __builtin_amdgcn_readfirstlane(max(lo, w0));
   const int e = __builtin_amdgcn_readfirstlane(min(L, w0 + WT));
 
   const int BS = p.block_size;
-  const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;  // elements per key row
+  const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + kh * D;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + kh * D;
   const int32_t* bt = p.block_table + b * p.max_blocks;
   const int qh0 = kh * G;
 
-  float m_run[4], l_run[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    m_run[j] = -INFINITY;
-    l_run[j] = 0.f;
-  }
-  float acc[G][8];
-#pragma unroll
-  for (int q = 0; q < G; ++q)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[q][i] = 0.f;
+  uint4* s_k = reinterpret_cast<uint4*>(smem + wave * WAVE_BYTES);  // [16][CH], swizzled
+  char* s_v = smem + wave * WAVE_BYTES + KBYTES;                    // [32][VRS]
 
-  // Lanes that own LDS probability columns: C rows 4*grp+j with 4*grp+j < G.
-  const bool writer = 4 * grp < G;
+  float m_q = -INFINITY, l_q = 0.f;  // running max / this lane's partial sum, query slot r16
+  floatx4 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   if (a < e) {
-    // A operand: query (r16 % G) of this kv head's group, chunk grp + 4*kk.
     const uint16_t* qrow = static_cast<const uint16_t*>(p.q) +
                            (static_cast<int64_t>(b) * p.num_heads + qh0 + r16 % G) * D;
-    uint4 qa[KK];
+    uint4 qb[KK];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
-      qa[kk] = *reinterpret_cast<const uint4*>(qrow + 8 * (grp + 4 * kk));
+      qb[kk] = *reinterpret_cast<const uint4*>(qrow + 8 * (grp + 4 * kk));
 
-    // Tile t covers keys [w0 + 16t, w0 + 16t + 16).  Loads are clamped to the
-    // valid tiles [a & ~15, (e-1) & ~15] (a clamped tile re-reads one already
-    // fetched: an L2 hit) and the compute masks keys outside [a, e), so the
-    // whole walk is straight-line code: the next tile's K/V loads stay in
-    // flight while the current tile computes.
     const int first_tile = a & ~15;
     const int last_tile = (e - 1) & ~15;
     uint4 kst[2][VL], vst[2][VL];
     auto load_tile = [&](int t, uint4 (&kr)[VL], uint4 (&vr)[VL]) {
       const int tt = __builtin_amdgcn_readfirstlane(min(max(w0 + 16 * t, first_tile), last_tile));
-      // Block ids outside [0, num_blocks) are clamped: the output is then
-      // meaningless but no access leaves the cache.
       const int blk = min(max(bt[tt / BS], 0), p.num_blocks - 1);
       const int64_t row0 = static_cast<int64_t>(blk) * BS + tt % BS;
-      // K and V alike: 16 lanes cover one 256-byte head row, RPL rows per
-      // instruction, the shape that streams at full HBM rate.
       const uint16_t* kp = kbase + (row0 + vrow) * row_stride + 8 * vch;
       const uint16_t* vp = vbase + (row0 + vrow) * row_stride + 8 * vch;
 #pragma unroll
@@ -297,6 +272,8 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
       for (int j = 0; j < VL; ++j) vr[j] = load_kv16(vp + RPL * j * row_stride);
     };
 
+    float p_even[4] = {0.f, 0.f, 0.f, 0.f};
+    float alpha_even = 1.f;
     load_tile(0, kst[0], vst[0]);
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
@@ -304,132 +281,108 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
       const uint4(&kr)[VL] = kst[t & 1];
       const uint4(&vr)[VL] = vst[t & 1];
       const int tt = w0 + 16 * t;
-
-      // K tile -> LDS (row vrow + RPL*j, chunk vch), read back in the MFMA B
-      // layout (key r16, chunk grp + 4*kk).  The strip is private to the wave
-      // and one wave's LDS operations complete in order.
-#pragma unroll
-      for (int j = 0; j < VL; ++j) {
-        const int row = vrow + RPL * j;
-        s_k[wave][row][vch ^ (row % CH)] = kr[j];
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-      // Scores of key tt + r16 for C rows j, in the log2 domain.
-      floatx4 sc = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk)
-        sc = mfma16x16x32(Tag{}, qa[kk], s_k[wave][r16][(grp + 4 * kk) ^ (r16 % CH)], sc);
-      const int tok = tt + r16;
-      const bool valid = tok >= a && tok < e;
-      float alpha[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float x = valid ? sc[j] * p.scale_log2 : -INFINITY;
-        const float mnew = fmaxf(m_run[j], row16_max(x));
-        const float msafe = mnew == -INFINITY ? 0.f : mnew;
-        alpha[j] = __builtin_amdgcn_exp2f(m_run[j] - msafe);
-        const float pr = __builtin_amdgcn_exp2f(x - msafe);
-        sc[j] = pr;
-        l_run[j] = l_run[j] * alpha[j] + pr;
-        m_run[j] = mnew;
-      }
-      if (writer) {
-        if (G >= 4) {
-          *reinterpret_cast<floatx4*>(&s_p[wave][r16][4 * grp]) = sc;
-        } else {
-#pragma unroll
-          for (int j = 0; j < G; ++j) s_p[wave][r16][j] = sc[j];
-        }
-        if (r16 == 0) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            if (4 * grp + j < G) s_alpha[wave][4 * grp + j] = alpha[j];
-        }
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-
-      // PV on the VALU: this lane's V chunk (8 d values) for rows vrow + RPL*j.
-#pragma unroll
-      for (int q = 0; q < G; ++q) {
-        const float al = s_alpha[wave][q];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[q][i] *= al;
-      }
       const bool full = tt >= a && tt + 16 <= e;
+
+      // K tile and V rows (keys outside [a, e) zeroed) into the wave's LDS.
 #pragma unroll
       for (int j = 0; j < VL; ++j) {
         const int row = vrow + RPL * j;
-        float pq[GP];
-        if (G >= 4) {
-#pragma unroll
-          for (int q4 = 0; q4 < G; q4 += 4) {
-            const floatx4 x = *reinterpret_cast<const floatx4*>(&s_p[wave][row][q4]);
-            pq[q4] = x[0];
-            pq[q4 + 1] = x[1];
-            pq[q4 + 2] = x[2];
-            pq[q4 + 3] = x[3];
-          }
-        } else {
-#pragma unroll
-          for (int q = 0; q < G; ++q) pq[q] = s_p[wave][row][q];
-        }
+        s_k[row * CH + (vch ^ (row % CH))] = kr[j];
         uint4 w = vr[j];
         if (!full) {
-          // Keys outside [a, e) carry p = 0; zero their V so stale or
-          // re-read cache contents (possibly NaN) cannot leak in via 0 * NaN.
           const int vt = tt + row;
           if (vt < a || vt >= e) w = make_uint4(0, 0, 0, 0);
         }
-        float vf[8];
-        unpack2(Tag{}, w.x, vf[0], vf[1]);
-        unpack2(Tag{}, w.y, vf[2], vf[3]);
-        unpack2(Tag{}, w.z, vf[4], vf[5]);
-        unpack2(Tag{}, w.w, vf[6], vf[7]);
+        *reinterpret_cast<uint4*>(s_v + ((t & 1) * 16 + row) * VRS + 16 * vch) = w;
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+      floatx4 sc = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int q = 0; q < G; ++q)
+      for (int kk = 0; kk < KK; ++kk)
+        sc = mfma16x16x32(Tag{}, s_k[r16 * CH + ((grp + 4 * kk) ^ (r16 % CH))], qb[kk], sc);
+
+      float x[4];
+      float mt = -INFINITY;
 #pragma unroll
-          for (int i = 0; i < 8; ++i) acc[q][i] = fmaf(pq[q], vf[i], acc[q][i]);
+      for (int j = 0; j < 4; ++j) {
+        const int tok = tt + 4 * grp + j;
+        x[j] = (tok >= a && tok < e) ? sc[j] * p.scale_log2 : -INFINITY;
+        mt = fmaxf(mt, x[j]);
+      }
+      mt = fmaxf(mt, __shfl_xor(mt, 16));
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float mnew = fmaxf(m_q, mt);
+      const float msafe = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = __builtin_amdgcn_exp2f(m_q - msafe);
+      float pr[4];
+      float psum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        pr[j] = __builtin_amdgcn_exp2f(x[j] - msafe);
+        psum += pr[j];
+      }
+      l_q = l_q * alpha + psum;
+      m_q = mnew;
+
+      if ((t & 1) == 0) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) p_even[j] = pr[j];
+        alpha_even = alpha;
+      } else {
+        // One 32-key PV step.  Rescale the accumulators (rows = query slots
+        // 4*grp + j, whose factors live in lanes 4*grp + j) and the even
+        // tile's probabilities to the current maximum.
+        const float apair = alpha_even * alpha;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float ar = __shfl(apair, 4 * grp + j);
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) acc[dt][j] *= ar;
+        }
+        uint4 pa;
+        pa.x = pack2(Tag{}, p_even[0] * alpha, p_even[1] * alpha);
+        pa.y = pack2(Tag{}, p_even[2] * alpha, p_even[3] * alpha);
+        pa.z = pack2(Tag{}, pr[0], pr[1]);
+        pa.w = pack2(Tag{}, pr[2], pr[3]);
+        const char* vrow_even = s_v + (4 * grp + r16 / 4) * VRS + 8 * (r16 % 4);
+        const char* vrow_odd = vrow_even + 16 * VRS;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const uint2 lo2 = lds_read_tr16(vrow_even + 32 * dt);
+          const uint2 hi2 = lds_read_tr16(vrow_odd + 32 * dt);
+          acc[dt] = mfma16x16x32(Tag{}, pa, make_uint4(lo2.x, lo2.y, hi2.x, hi2.y), acc[dt]);
+        }
       }
       __builtin_amdgcn_wave_barrier();
     }
   }
 
-  // Wave totals: sum l over the 16 keys of a row; sum acc over V rows.
-#pragma unroll
-  for (int j = 0; j < 4; ++j) l_run[j] = row16_sum(l_run[j]);
-#pragma unroll
-  for (int q = 0; q < G; ++q)
-#pragma unroll
-    for (int i = 0; i < 8; ++i)
-#pragma unroll
-      for (int m = CH; m < 64; m <<= 1) acc[q][i] += __shfl_xor(acc[q][i], m);
+  // Wave totals: l summed over the 4 lane groups (every group then holds the
+  // slot's total); maxima are already equal across groups.
+  l_q += __shfl_xor(l_q, 16);
+  l_q += __shfl_xor(l_q, 32);
 
-  if (lane < CH) {
+  __syncthreads();  // the loop's LDS is reused by the epilogue
+  float* s_o = reinterpret_cast<float*>(smem);           // [kWaves][G][D]
+  float* s_m = s_o + kWaves * G * D;                      // [kWaves][G]
+  float* s_l = s_m + kWaves * G;                          // [kWaves][G]
 #pragma unroll
-    for (int q = 0; q < G; ++q) {
-      *reinterpret_cast<floatx4*>(&s_o[wave][q][8 * lane]) =
-          floatx4{acc[q][0], acc[q][1], acc[q][2], acc[q][3]};
-      *reinterpret_cast<floatx4*>(&s_o[wave][q][8 * lane + 4]) =
-          floatx4{acc[q][4], acc[q][5], acc[q][6], acc[q][7]};
+  for (int j = 0; j < 4; ++j) {
+    const int slot = 4 * grp + j;
+    if (slot < G) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) s_o[(wave * G + slot) * D + dt * 16 + r16] = acc[dt][j];
     }
   }
-  if (writer && r16 == 0) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (4 * grp + j < G) {
-        s_m[wave][4 * grp + j] = m_run[j];
-        s_l[wave][4 * grp + j] = l_run[j];
-      }
-    }
+  if (grp == 0 && r16 < G) {
+    s_m[wave * G + r16] = m_q;
+    s_l[wave * G + r16] = l_q;
   }
   __syncthreads();
 
-  // Combine the 4 waves: normalised split output o and its log2-sum-exp.
   const int first = lo / (kWaves * WT);
   const int nsplits = (L - 1) / (kWaves * WT) - first + 1;
   uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + qh0) * D;
@@ -439,18 +392,18 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
     const int d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][q]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w * G + q]);
     const float msafe = M == -INFINITY ? 0.f : M;
     float lsum = 0.f, osum = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float f = __builtin_amdgcn_exp2f(s_m[w][q] - msafe);
-      lsum += f * s_l[w][q];
-      osum += f * s_o[w][q][d];
+      const float f = __builtin_amdgcn_exp2f(s_m[w * G + q] - msafe);
+      lsum += f * s_l[w * G + q];
+      osum += f * s_o[(w * G + q) * D + d];
     }
     const float o = lsum > 0.f ? osum / lsum : 0.f;
     if (nsplits == 1) {
-      out[idx] = pack1(Tag{}, o);  // the only split: final output directly
+      out[idx] = pack1(Tag{}, o);
     } else {
       const int64_t prow = prow0 + static_cast<int64_t>(q) * p.max_splits + split;
       p.part_o[prow * D + d] = o;
@@ -541,17 +494,20 @@ dim3 split_grid(const DecodeParams& p) {
 #endif
 }
 
+template <class Tag, int D, int G, int TILES>
+void launch_tiles(const DecodeParams& p, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((paged_decode_split<Tag, D, G, TILES>), grid, dim3(kThreads), 0, s, p);
+}
+
 template <class Tag, int D, int G>
 void launch_split(const DecodeParams& p, int64_t batch, hipStream_t s) {
+  (void)batch;
   const dim3 grid = split_grid(p);
   // split_tokens = kWaves * 16 * TILES.
-  switch (p.split_tokens) {
-    case 256: hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 4>), grid, dim3(kThreads), 0, s, p); break;
-#if OXIDE_SPLIT_TOKENS == 1024
-    case 1024: hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 16>), grid, dim3(kThreads), 0, s, p); break;
-#endif
-    default: hipLaunchKernelGGL((paged_decode_split<Tag, D, G, 8>), grid, dim3(kThreads), 0, s, p); break;
-  }
+  if (p.split_tokens == 256)
+    launch_tiles<Tag, D, G, 4>(p, grid, s);
+  else
+    launch_tiles<Tag, D, G, 8>(p, grid, s);
 }
 
 template <class Tag, int D>
