@@ -412,30 +412,39 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
   }
 }
 
-// Pass 2: one wave per (query head, sequence) merges the splits that
-// intersect [lo, L) with log-sum-exp weights.  Sequences with a single split
-// were finished by pass 1 and are skipped; empty sequences get zeros.
+// Pass 2: one workgroup of 4 waves per (query head, sequence) merges the
+// splits that intersect [lo, L) with log-sum-exp weights; each wave takes a
+// contiguous quarter of the splits and the quarters are combined in LDS.
+// Sequences with a single split were finished by pass 1 and are skipped;
+// empty sequences get zeros.
 template <class Tag, int D>
-__global__ __launch_bounds__(64) void paged_decode_merge(DecodeParams p) {
+__global__ __launch_bounds__(kThreads) void paged_decode_merge(DecodeParams p) {
   constexpr int PER = D / 64;
+  __shared__ float s_o[kWaves][D];
+  __shared__ float s_mw[kWaves][2];
   const int h = blockIdx.x;
   const int b = blockIdx.y;
-  const int lane = threadIdx.x;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
   const int L = seq_len(p, b);
   uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + h) * D;
   if (L == 0) {
-#pragma unroll
-    for (int i = 0; i < PER; ++i) out[lane + 64 * i] = 0;
+    for (int i = threadIdx.x; i < D; i += kThreads) out[i] = 0;
     return;
   }
   const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
   const int first = lo / p.split_tokens;
   const int last = (L - 1) / p.split_tokens;
   if (first == last) return;
+  const int n = last - first + 1;
+  const int chunk = (n + kWaves - 1) / kWaves;
+  const int w_first = first + wave * chunk;
+  const int w_last = min(last, w_first + chunk - 1);
+
   const int64_t prow0 = (static_cast<int64_t>(b) * p.num_heads + h) * p.max_splits;
   const float* lse = p.part_lse + prow0;
   float M = -INFINITY;
-  for (int sp = first + lane; sp <= last; sp += 64) M = fmaxf(M, lse[sp]);
+  for (int sp = w_first + lane; sp <= w_last; sp += 64) M = fmaxf(M, lse[sp]);
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
   const float msafe = M == -INFINITY ? 0.f : M;
@@ -443,27 +452,52 @@ __global__ __launch_bounds__(64) void paged_decode_merge(DecodeParams p) {
 #pragma unroll
   for (int i = 0; i < PER; ++i) o[i] = 0.f;
   float wsum = 0.f;
-  // Splits in groups of 64: lane i owns the weight of split g + i, which every
+  // Groups of 64 splits: lane i owns the weight of split g + i, which every
   // lane reads with a scalar readlane while several partial rows are in flight.
-  for (int g = first; g <= last; g += 64) {
-    const int n = min(64, last - g + 1);
-    const float wl = lane < n ? __builtin_amdgcn_exp2f(lse[g + lane] - msafe) : 0.f;
+  for (int g = w_first; g <= w_last; g += 64) {
+    const int cnt = min(64, w_last - g + 1);
+    const float wl = lane < cnt ? __builtin_amdgcn_exp2f(lse[g + lane] - msafe) : 0.f;
     float ws = wl;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ws += __shfl_xor(ws, m);
     wsum += ws;
     const float* po = p.part_o + (prow0 + g) * D + lane;
 #pragma unroll 8
-    for (int i = 0; i < n; ++i) {
+    for (int i = 0; i < cnt; ++i) {
       const float w =
           __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i));
 #pragma unroll
       for (int k = 0; k < PER; ++k) o[k] = fmaf(w, po[static_cast<int64_t>(i) * D + 64 * k], o[k]);
     }
   }
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
 #pragma unroll
-  for (int i = 0; i < PER; ++i) out[lane + 64 * i] = pack1(Tag{}, o[i] * inv);
+  for (int k = 0; k < PER; ++k) s_o[wave][lane + 64 * k] = o[k];
+  if (lane == 0) {
+    s_mw[wave][0] = w_first <= w_last ? M : -INFINITY;
+    s_mw[wave][1] = wsum;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float Mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) Mt = fmaxf(Mt, s_mw[w][0]);
+    const float mt = Mt == -INFINITY ? 0.f : Mt;
+    float f[kWaves], wt = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = s_mw[w][0];
+      f[w] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mt);
+      wt += f[w] * s_mw[w][1];
+    }
+    const float inv = wt > 0.f ? 1.f / wt : 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) acc = fmaf(f[w], s_o[w][lane + 64 * k], acc);
+      out[lane + 64 * k] = pack1(Tag{}, acc * inv);
+    }
+  }
 }
 
 // Zero output for a batch whose max_seqlen_k is 0 (no split workgroups run).
@@ -534,12 +568,12 @@ bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hip
   const dim3 mgrid(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(batch));
   if (head_dim == 128) {
     if (!dispatch_group<Tag, 128>(p, batch, group, s)) return false;
-    hipLaunchKernelGGL((paged_decode_merge<Tag, 128>), mgrid, dim3(64), 0, s, p);
+    hipLaunchKernelGGL((paged_decode_merge<Tag, 128>), mgrid, dim3(kThreads), 0, s, p);
     return true;
   }
   if (head_dim == 64) {
     if (!dispatch_group<Tag, 64>(p, batch, group, s)) return false;
-    hipLaunchKernelGGL((paged_decode_merge<Tag, 64>), mgrid, dim3(64), 0, s, p);
+    hipLaunchKernelGGL((paged_decode_merge<Tag, 64>), mgrid, dim3(kThreads), 0, s, p);
     return true;
   }
   return false;
