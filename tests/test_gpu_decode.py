@@ -5,10 +5,7 @@ max-abs 2e-2 and max-rel 1e-2, checked by helpers.assert_attn_close.  The oracle
 (oracle/oxide_oracle.c, fp32 accumulate) is itself pinned against numpy fp64 in
 tests/test_oracle.py.
 """
-import json
 import math
-from pathlib import Path
-
 import numpy as np
 import pytest
 
@@ -193,3 +190,76 @@ def test_decode_workspace_reuse_across_shapes(device):
             fresh = to_bits(ox.decode_attn(*args))
             torch.cuda.synchronize()
             assert np.array_equal(shared, fresh), (rep, i)
+
+
+def _full_size_inputs(cfg_id, seed, device):
+    import torch
+    from oxide_paged_kv.workload import CONFIGS, make_decode_step
+
+    st = make_decode_step(CONFIGS[cfg_id], seed=seed)
+    c = st.cfg
+    g = torch.Generator(device=device).manual_seed(seed)
+    shape = (st.pool_blocks, c.block_size, c.num_kv_heads, c.head_dim)
+    kc = torch.randn(shape, generator=g, device=device).bfloat16()
+    vc = torch.randn(shape, generator=g, device=device).bfloat16()
+    q = torch.randn((c.batch, c.num_heads, c.head_dim), generator=g, device=device).bfloat16()
+    return st, kc, vc, q
+
+
+def _check_sampled(st, kc, vc, q, out, samples, window=-1):
+    """Oracle on the sampled sequences' own blocks (gathered to the host)."""
+    import torch
+
+    scale = 1 / math.sqrt(st.cfg.head_dim)
+    for b in samples:
+        rows = st.block_rows[b]
+        ids = torch.from_numpy(np.asarray(rows, np.int64)).to(kc.device)
+        kb, vb = to_bits(kc[ids]), to_bits(vc[ids])
+        L = int(st.context_lens[b])
+        want = oracle.paged_decode_attention(
+            to_bits(q[b:b + 1]), kb, vb, np.array([0, L], np.uint32),
+            np.arange(len(rows), dtype=np.int32)[None], scale, window, threads=16)
+        assert_attn_close(out[b:b + 1], want)
+
+
+def test_decode_cfg4_prefix_cow_window_full_size(device):
+    """cfg4 at full size: 128 sequences share a 4096-token prefix (16 blocks); the
+    last shared block is copied per sequence with copy_blocks (copy-on-write), each
+    sequence appends its new token, then decode attention with window 4096."""
+    import torch
+    import oxide_paged_kv as ox
+
+    st, kc, vc, q = _full_size_inputs(4, 41, device)
+    c = st.cfg
+    print(f"cfg4 B={c.batch} pool={st.pool_blocks} cow_pairs={len(st.cow_pairs)}", flush=True)
+    pairs = torch.from_numpy(st.cow_pairs).to(device)
+    ox.copy_blocks(kc, vc, pairs)
+    knew = torch.randn((c.batch, c.num_kv_heads, c.head_dim), device=device).bfloat16()
+    vnew = torch.randn_like(knew, dtype=torch.float32).bfloat16()
+    ox.reshape_and_cache(knew, vnew, kc, vc, torch.from_numpy(st.slot_mapping).to(device))
+    cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
+    bt = torch.from_numpy(st.block_table).to(device)
+    out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim),
+                                c.window_left))
+    # CoW copies are bit-exact, and every sequence's private copy equals the shared block.
+    src, dst = pairs[:, 0], pairs[:, 1]
+    # (the appended tokens sit past the prefix, so the copies are still intact)
+    assert torch.equal(kc[dst].view(torch.int16), kc[src].view(torch.int16))
+    assert torch.equal(vc[dst].view(torch.int16), vc[src].view(torch.int16))
+    _check_sampled(st, kc, vc, q, out, [0, 37, 127], c.window_left)
+
+
+def test_decode_cfg5_long_context_full_size(device):
+    """cfg5 at full size: Qwen3-32B decode shape (G = 8), 16 sequences of 32k-128k
+    keys; the longest and the shortest sequences are checked against the oracle."""
+    import torch
+    import oxide_paged_kv as ox
+
+    st, kc, vc, q = _full_size_inputs(5, 51, device)
+    c = st.cfg
+    print(f"cfg5 B={c.batch} pool={st.pool_blocks} max_len={st.max_seqlen_k}", flush=True)
+    cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
+    bt = torch.from_numpy(st.block_table).to(device)
+    out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim)))
+    lens = st.context_lens.astype(np.int64)
+    _check_sampled(st, kc, vc, q, out, [int(lens.argmax()), int(lens.argmin())])
