@@ -142,6 +142,20 @@ size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
 int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
                                             int64_t max_seqlen_k);
 
+/*
+ * Decode metadata on the device (the reference builds it on the host in every
+ * layer: crates/vllm-oxide/src/engine/mod.rs:247-267, metadata.rs:20-47,
+ * kv_cache_manager.rs:115-135).  From context_lens (uint32 [batch], the new
+ * token included) and the 0-padded int32 block table [batch, max_blocks_per_seq]:
+ *   cu_seqlens_k[0] = 0, cu_seqlens_k[b+1] = cu_seqlens_k[b] + context_lens[b]
+ *   slot_mapping[b] = block_table[b][(L-1)/block_size] * block_size + (L-1) % block_size,
+ *                     L = context_lens[b]; -1 when L == 0 or (L-1)/block_size >= max_blocks_per_seq.
+ * One small launch; batch <= 65535.
+ */
+void build_decode_metadata_device(const uint32_t* context_lens, const int32_t* block_table,
+                                  int64_t max_blocks_per_seq, int64_t batch, int64_t block_size,
+                                  uint32_t* cu_seqlens_k, int64_t* slot_mapping, void* stream);
+
 /* Error state of the calling host thread: the first error since the last
  * oxide_clear_error(), or OXIDE_OK. */
 int oxide_last_error(void);

@@ -5,5 +5,5 @@ vllm-oxide_amd/build.py); this package only binds them (ctypes) and generates
 the synthetic workloads of the benchmark configurations.
 """
 from ._lib import LIB_PATH, OxideError, load  # noqa: F401
-from .ops import (copy_blocks, decode_attn, dtype_code, gather_blocks,  # noqa: F401
+from .ops import (build_decode_metadata, copy_blocks, decode_attn, dtype_code, gather_blocks,  # noqa: F401
                   reshape_and_cache, split_tokens, workspace_size)

@@ -131,3 +131,21 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         _stream(q))
     _lib.check()
     return out
+
+
+def build_decode_metadata(context_lens: torch.Tensor, block_table: torch.Tensor, block_size: int = 256):
+    """Device-side decode metadata: (cu_seqlens_k [B+1] as int32 bits of uint32,
+    slot_mapping int64 [B]) from context_lens (int32 bits of uint32, [B]) and the
+    0-padded int32 block table [B, max_blocks]."""
+    L = _lib.load()
+    if context_lens.dtype not in (torch.int32, torch.uint32) or block_table.dtype != torch.int32:
+        raise _lib.OxideError("context_lens must be 32-bit and block_table int32")
+    B = context_lens.shape[0]
+    cu = torch.empty(B + 1, dtype=torch.int32, device=context_lens.device)
+    slots = torch.empty(B, dtype=torch.int64, device=context_lens.device)
+    max_blocks = block_table.shape[1] if block_table.dim() == 2 else 0
+    L.build_decode_metadata_device(_ptr(context_lens), _ptr(block_table) if block_table.numel() else None,
+                                   max_blocks, B, block_size, _ptr(cu), _ptr(slots) if B else None,
+                                   _stream(context_lens))
+    _lib.check()
+    return cu, slots
