@@ -32,7 +32,7 @@ sys.path.insert(0, str(REPO))
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary of the same workload (calibrated HBM
 # bytes per attention call); the committed summary names the config it covers.
-TRAFFIC_PROFILE = {3: REPO / "profiles" / "paged_decode_cfg3.md"}
+TRAFFIC_PROFILE = {3: REPO / "profiles" / "paged_decode_cfg3.md", 5: REPO / "profiles" / "paged_decode_cfg5.md"}
 
 
 def profiled_traffic(config: int):
