@@ -263,3 +263,26 @@ def test_decode_cfg5_long_context_full_size(device):
     out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim)))
     lens = st.context_lens.astype(np.int64)
     _check_sampled(st, kc, vc, q, out, [int(lens.argmax()), int(lens.argmin())])
+
+
+@pytest.mark.parametrize("batch,ctx_hi,want_split", [(64, 4096, 512), (64, 8192, 1024), (8, 3000, 256)])
+def test_decode_each_split_size_sampled(device, batch, ctx_hi, want_split):
+    """One batch per split size the policy picks (256, 512 and 1024 keys per
+    workgroup), Qwen3-8B heads, sampled sequences checked against the oracle."""
+    import torch
+    import oxide_paged_kv as ox
+    from oxide_paged_kv.workload import DecodeConfig, make_decode_step
+
+    cfg = DecodeConfig(f"split{want_split}", 32, 8, 128, batch, 1, ctx_hi, 0)
+    st = make_decode_step(cfg, seed=want_split)
+    assert ox.split_tokens(batch, 8, st.max_seqlen_k) == want_split
+    g = torch.Generator(device=device).manual_seed(want_split)
+    shape = (st.pool_blocks, 256, 8, 128)
+    kc = torch.randn(shape, generator=g, device=device).bfloat16()
+    vc = torch.randn(shape, generator=g, device=device).bfloat16()
+    q = torch.randn((batch, 32, 128), generator=g, device=device).bfloat16()
+    cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
+    bt = torch.from_numpy(st.block_table).to(device)
+    out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(128)))
+    lens = st.context_lens.astype(np.int64)
+    _check_sampled(st, kc, vc, q, out, sorted({0, int(lens.argmax()), int(lens.argmin()), batch - 1}))

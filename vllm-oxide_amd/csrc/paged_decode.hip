@@ -47,7 +47,7 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // Build-time tuning knobs (defaults are the tuned values).
 #ifndef OXIDE_SPLIT_TOKENS
-#define OXIDE_SPLIT_TOKENS 0  // 0 = policy in choose_split_tokens
+#define OXIDE_SPLIT_TOKENS 0  // 0 = policy in choose_split_tokens; else 256, 512 or 1024
 #endif
 #ifndef OXIDE_DECODE_WAVES_PER_EU
 #define OXIDE_DECODE_WAVES_PER_EU 0  // >0: ask the compiler for this occupancy
@@ -510,11 +510,16 @@ __global__ __launch_bounds__(256) void zero_fill_u16(uint16_t* out, int64_t n) {
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 int64_t choose_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
-  // 512-key splits keep the partials under 2% of the K/V bytes; fall back to
-  // 256 when that would leave too few workgroups to fill 256 CUs.
-  const int64_t wgs512 = batch * num_kv_heads * ceil_div(max_seqlen_k, 512);
+  // The longest split (fewest partials, shortest merge) that still yields at
+  // least 4096 workgroups -- about eight per workgroup slot of the 256 CUs --
+  // so that the ragged tail of the grid stays short.  Measured on MI355X:
+  // Qwen3-8B B=64 ctx 2k-8k and Qwen3-32B B=16 ctx 32k-128k are fastest at
+  // 1024, Qwen3-0.6B B=32 ctx 0.5k-4k at 256.
   if (OXIDE_SPLIT_TOKENS > 0) return OXIDE_SPLIT_TOKENS;
-  return wgs512 >= 4096 ? 512 : 256;
+  for (int64_t st : {int64_t{1024}, int64_t{512}}) {
+    if (batch * num_kv_heads * ceil_div(max_seqlen_k, st) >= 4096) return st;
+  }
+  return 256;
 }
 
 dim3 split_grid(const DecodeParams& p) {
@@ -540,6 +545,8 @@ void launch_split(const DecodeParams& p, int64_t batch, hipStream_t s) {
   // split_tokens = kWaves * 16 * TILES.
   if (p.split_tokens == 256)
     launch_tiles<Tag, D, G, 4>(p, grid, s);
+  else if (p.split_tokens == 1024)
+    launch_tiles<Tag, D, G, 16>(p, grid, s);
   else
     launch_tiles<Tag, D, G, 8>(p, grid, s);
 }
