@@ -2,7 +2,9 @@
 
 A step is one layer's decode-time work on the paged cache, in the reference's
 order (models/qwen3.rs:199-208): KV append of one new token per sequence
-(reshape_and_cache), then paged decode attention over every sequence's context.
+(reshape_and_cache), then paged decode attention over every sequence's context --
+by default in one launch (paged_decode_attention_append), with --separate as the
+two calls of the reference.
 Default workload: BASELINE config 3 (Qwen3-8B shape, 32 q / 8 kv heads, D 128,
 bf16, block 256, batch 64, context U[2048, 8192], 8192-block pool), synthetic
 N(0,1) data resident in HBM, steps rotating over distinct layers of the
@@ -32,11 +34,12 @@ sys.path.insert(0, str(REPO))
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary of the same workload (calibrated HBM
 # bytes per attention call); the committed summary names the config it covers.
-TRAFFIC_PROFILE = {3: REPO / "profiles" / "paged_decode_cfg3.md", 5: REPO / "profiles" / "paged_decode_cfg5.md"}
+TRAFFIC_PROFILE = {(3, False): REPO / "profiles" / "paged_decode_cfg3.md",
+                   (5, False): REPO / "profiles" / "paged_decode_cfg5.md"}
 
 
-def profiled_traffic(config: int):
-    path = TRAFFIC_PROFILE.get(config)
+def profiled_traffic(config: int, separate: bool):
+    path = TRAFFIC_PROFILE.get((config, separate))
     if path is None or not path.exists():
         return None
     for line in path.read_text().splitlines():
@@ -99,7 +102,8 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=0, help="distinct layers to rotate over (0 = auto)")
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--stream-copy", action="store_true", default=True)
+    ap.add_argument("--separate", action="store_true",
+                    help="append and attention as two calls (default: one fused call)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -141,10 +145,17 @@ def main() -> int:
         kc, vc = buf[0, layer], buf[1, layer]
         if ev:
             ev[0].record()
-        ox.reshape_and_cache(knew[layer], vnew[layer], kc, vc, sm)
-        if ev:
-            ev[1].record()
-        ox.decode_attn(q[layer], kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out, workspace=ws)
+        if args.separate:
+            ox.reshape_and_cache(knew[layer], vnew[layer], kc, vc, sm)
+            if ev:
+                ev[1].record()
+            ox.decode_attn(q[layer], kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out,
+                           workspace=ws)
+        else:
+            if ev:
+                ev[1].record()
+            ox.decode_attn(q[layer], kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out,
+                           workspace=ws, append=(knew[layer], vnew[layer], sm))
         if ev:
             ev[2].record()
 
@@ -158,33 +169,46 @@ def main() -> int:
         step(args.warmup + i, evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    app_ms = [e[0].elapsed_time(e[1]) for e in evs]
     att_ms = [e[1].elapsed_time(e[2]) for e in evs]
     ms_per_step = wall * 1e3 / args.steps
     attn_bytes, app_bytes = st.attn_bytes(), st.append_bytes()
     attn_us = float(np.mean(att_ms)) * 1e3
-    app_us = float(np.mean(app_ms)) * 1e3
-    attn_gbps = attn_bytes / (attn_us * 1e-6) / 1e9
-    app_gbps = app_bytes / (app_us * 1e-6) / 1e9
+    # The timed call's algorithmic bytes: attention, plus the append when fused into it.
+    call_bytes = attn_bytes if args.separate else attn_bytes + app_bytes
+    attn_gbps = call_bytes / (attn_us * 1e-6) / 1e9
     value = (attn_bytes + app_bytes) / (ms_per_step * 1e-3) / 1e9
+    # The append kernel on its own (reshape_and_cache), for append GB/s.  A few
+    # attention calls are queued first so the GPU is still busy while the host
+    # enqueues the short appends: the events then time the device, not the launches.
+    for i in range(8):
+        ox.decode_attn(q[i % layers], buf[0, i % layers], buf[1, i % layers], cu, bt, st.max_seqlen_k,
+                       scale, window, BS, out=out, workspace=ws)
+    a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a0.record()
+    for i in range(20):
+        layer = i % layers
+        ox.reshape_and_cache(knew[layer], vnew[layer], buf[0, layer], buf[1, layer], sm)
+    a1.record()
+    torch.cuda.synchronize()
+    app_us = a0.elapsed_time(a1) / 20 * 1e3
+    app_gbps = app_bytes / (app_us * 1e-6) / 1e9
 
     extra = {}
-    if args.stream_copy:
-        # Achievable-bandwidth calibration: copy_blocks over 1 MiB blocks (read+write).
-        nblk = 2048
-        cbuf = torch.empty((2, 2 * nblk, BS, H, D), dtype=torch.bfloat16, device=dev)
-        pairs = torch.stack([torch.arange(nblk), torch.arange(nblk, 2 * nblk)], 1).to(dev)
-        for _ in range(3):
-            ox.copy_blocks(cbuf[0], cbuf[1], pairs)
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(10):
-            ox.copy_blocks(cbuf[0], cbuf[1], pairs)
-        e1.record()
-        torch.cuda.synchronize()
-        cbytes = 2 * nblk * 2 * (BS * H * D * 2)
-        extra["stream_copy_gbps"] = round(cbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9, 1)
-        del cbuf
+    # Achievable-bandwidth calibration: copy_blocks over 1 MiB blocks (read+write).
+    nblk = 2048
+    cbuf = torch.empty((2, 2 * nblk, BS, H, D), dtype=torch.bfloat16, device=dev)
+    pairs = torch.stack([torch.arange(nblk), torch.arange(nblk, 2 * nblk)], 1).to(dev)
+    for _ in range(3):
+        ox.copy_blocks(cbuf[0], cbuf[1], pairs)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(10):
+        ox.copy_blocks(cbuf[0], cbuf[1], pairs)
+    e1.record()
+    torch.cuda.synchronize()
+    cbytes = 2 * nblk * 2 * (BS * H * D * 2)
+    extra["stream_copy_gbps"] = round(cbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9, 1)
+    del cbuf
 
     res = {
         "metric": "paged-decode attn KV-read GB/s (% HBM peak) + append GB/s, Qwen3-8B shape",
@@ -204,6 +228,7 @@ def main() -> int:
                    "ctx": [cfg.ctx_lo, cfg.ctx_hi], "window_left": cfg.window_left,
                    "layers_rotated": layers, "split_tokens": ox.split_tokens(cfg.batch, H, st.max_seqlen_k),
                    "total_keys": int(st.context_lens.sum())},
+        "step_mode": "separate append + attention" if args.separate else "fused append + attention (one launch)",
         "attn_us": round(attn_us, 2),
         "attn_kv_read_gbps": round(st.kv_read_bytes() / (attn_us * 1e-6) / 1e9, 1),
         "attn_gbps": round(attn_gbps, 1),
@@ -213,9 +238,10 @@ def main() -> int:
         "tokens_per_s": round(cfg.batch / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": profiled_traffic(args.config),
-                     "kernel": "paged_decode_split + paged_decode_merge (one attention call)",
-                     "algorithmic_bytes": attn_bytes},
+                     "traffic": profiled_traffic(args.config, args.separate),
+                     "kernel": "paged_decode_split + paged_decode_merge (one attention call"
+                               + ("" if args.separate else ", append fused") + ")",
+                     "algorithmic_bytes": call_bytes},
         **extra,
     }
     if not args.no_cpu_baseline:

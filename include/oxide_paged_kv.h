@@ -133,6 +133,29 @@ void paged_decode_attention(void* out, const void* q, const void* k_cache, const
                             int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
                             void* workspace, size_t workspace_bytes, int dtype, void* stream);
 
+/*
+ * KV append fused into the decode attention launch: the same result as
+ *   reshape_and_cache(key, value, k_cache, v_cache, slot_mapping, batch,
+ *                     num_kv_heads, head_dim, dtype, stream);
+ *   paged_decode_attention(out, q, k_cache, v_cache, ...);
+ * (the append-then-attend order of models/qwen3.rs:199-208) in one launch.
+ * key / value: [batch, num_kv_heads, head_dim], one new token per sequence;
+ * slot_mapping[b] must be -1 or the cache slot of key L_b - 1 of sequence b,
+ * which is what compute_slot_mapping gives at decode
+ * (kv_cache_manager.rs:115-135, engine/mod.rs:250-257).  The workgroup that
+ * attends to key L_b - 1 writes its kv head's slice of the new row and uses
+ * it directly, so no extra ordering is needed.  Other arguments as for
+ * paged_decode_attention (the same workspace size).
+ */
+void paged_decode_attention_append(void* out, const void* q, const void* key, const void* value,
+                                   const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                                   const uint32_t* cu_seqlens_k, const int32_t* block_table,
+                                   int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
+                                   int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                   int64_t page_block_size, int64_t max_seqlen_k,
+                                   int32_t window_left, float softmax_scale, void* workspace,
+                                   size_t workspace_bytes, int dtype, void* stream);
+
 /* Bytes of workspace paged_decode_attention needs for these arguments. */
 size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
                                              int64_t num_kv_heads, int64_t head_dim,

@@ -286,3 +286,72 @@ def test_decode_each_split_size_sampled(device, batch, ctx_hi, want_split):
     out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(128)))
     lens = st.context_lens.astype(np.int64)
     _check_sampled(st, kc, vc, q, out, sorted({0, int(lens.argmax()), int(lens.argmin()), batch - 1}))
+
+
+FUSED_CASES = [
+    # (B, Hq, Hkv, D, BS, NB, lens, window, dtype)
+    (4, 16, 8, 128, 256, 64, [300, 1000, 557, 999], -1, "bf16"),
+    (3, 64, 8, 128, 256, 80, [9000, 513, 1], -1, "bf16"),
+    (5, 16, 8, 128, 256, 20, [0, 10, 0, 1, 300], -1, "bf16"),
+    (2, 4, 2, 64, 16, 200, [700, 33], 100, "f16"),
+    (4, 32, 8, 128, 256, 64, [5000, 4097, 100, 4096], 4096, "bf16"),
+]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=[f"f{i}" for i in range(len(FUSED_CASES))])
+def test_decode_fused_append_equals_append_then_attend(device, case):
+    """paged_decode_attention_append == reshape_and_cache + paged_decode_attention,
+    bit for bit (output and caches); slot -1 skips the append."""
+    import torch
+    import oxide_paged_kv as ox
+
+    B, Hq, Hkv, D, BS, NB, lens, window, dtype = case
+    q, kc, vc, cu, table, mx = _case(31, B, Hq, Hkv, D, BS, NB, lens, dtype)
+    rng = np.random.default_rng(32)
+    knew = normal_bits(rng, (B, Hkv, D), dtype)
+    vnew = normal_bits(rng, (B, Hkv, D), dtype)
+    used = {int(table[b, i]) for b, L in enumerate(lens) for i in range((L + BS - 1) // BS)}
+    spare = [blk for blk in range(NB) if blk not in used]
+    # Sequences with no keys append into distinct spare blocks (distinct slots: the
+    # reference kernel's result is undefined when two tokens share a slot).
+    slots = np.array([table[b, (L - 1) // BS] * BS + (L - 1) % BS if L > 0 else spare[b] * BS + 3
+                      for b, L in enumerate(lens)], np.int64)
+    slots[1 % B] = -1  # one sequence skips its append
+    args = lambda k, v: (to_torch(q, dtype, device), k, v, torch.from_numpy(cu.view(np.int32)).to(device),
+                         torch.from_numpy(table).to(device), mx, 1 / math.sqrt(D),
+                         None if window < 0 else window, BS)
+    k1, v1 = to_torch(kc, dtype, device), to_torch(vc, dtype, device)
+    kn, vn, sm = to_torch(knew, dtype, device), to_torch(vnew, dtype, device), torch.from_numpy(slots).to(device)
+    ox.reshape_and_cache(kn, vn, k1, v1, sm)
+    want = to_bits(ox.decode_attn(*args(k1, v1)))
+    k2, v2 = to_torch(kc, dtype, device), to_torch(vc, dtype, device)
+    got = to_bits(ox.decode_attn(*args(k2, v2), append=(kn, vn, sm)))
+    torch.cuda.synchronize()
+    assert np.array_equal(got, want)
+    assert np.array_equal(to_bits(k2), to_bits(k1))
+    assert np.array_equal(to_bits(v2), to_bits(v1))
+
+
+@pytest.mark.parametrize("cfg_id", [3, 5])
+def test_decode_fused_append_full_size(device, cfg_id):
+    """Full-size cfg3 / cfg5 step: fused append + attention equals the two calls."""
+    import torch
+    import oxide_paged_kv as ox
+
+    st, kc, vc, q = _full_size_inputs(cfg_id, 60 + cfg_id, device)
+    c = st.cfg
+    g = torch.Generator(device=device).manual_seed(cfg_id)
+    kn = torch.randn((c.batch, c.num_kv_heads, c.head_dim), generator=g, device=device).bfloat16()
+    vn = torch.randn((c.batch, c.num_kv_heads, c.head_dim), generator=g, device=device).bfloat16()
+    sm = torch.from_numpy(st.slot_mapping).to(device)
+    cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
+    bt = torch.from_numpy(st.block_table).to(device)
+    scale = 1 / math.sqrt(c.head_dim)
+    k2, v2 = kc.clone(), vc.clone()
+    ox.reshape_and_cache(kn, vn, kc, vc, sm)
+    want = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale)
+    got = ox.decode_attn(q, k2, v2, cu, bt, st.max_seqlen_k, scale, append=(kn, vn, sm))
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert torch.equal(k2.view(torch.int16), kc.view(torch.int16))
+    assert torch.equal(v2.view(torch.int16), vc.view(torch.int16))

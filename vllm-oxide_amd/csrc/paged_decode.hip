@@ -105,6 +105,11 @@ struct DecodeParams {
   float* part_o;    // [B, Hq, max_splits, D]
   float* part_lse;  // [B, Hq, max_splits]
   void* out;        // [B, Hq, D]
+  // Fused append (paged_decode_attention_append), null otherwise: the new
+  // token's K/V [B, Hkv, D] and its slot per sequence.
+  const void* new_k;
+  const void* new_v;
+  const int64_t* slot_mapping;
   int64_t max_blocks;
   int num_blocks;
   int max_seqlen_k;
@@ -272,6 +277,15 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
       for (int j = 0; j < VL; ++j) vr[j] = load_kv16(vp + RPL * j * row_stride);
     };
 
+    // Fused append: the wave whose keys include the new token (key L - 1)
+    // writes this kv head's slice of the token's K/V row to its slot and uses
+    // it in place of the row it loaded from the cache.  No other workgroup
+    // reads that slice, so no ordering with other workgroups is needed.
+    const int key_new = L - 1;
+    int64_t slot_new = -1;
+    if (p.new_k != nullptr) slot_new = p.slot_mapping[b];
+    const bool owns_new = slot_new >= 0 && key_new >= a && key_new < e;
+
     float p_even[4] = {0.f, 0.f, 0.f, 0.f};
     float alpha_even = 1.f;
     load_tile(0, kst[0], vst[0]);
@@ -294,6 +308,19 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
           if (vt < a || vt >= e) w = make_uint4(0, 0, 0, 0);
         }
         *reinterpret_cast<uint4*>(s_v + ((t & 1) * 16 + row) * VRS + 16 * vch) = w;
+      }
+      if (owns_new && key_new >= tt && key_new < tt + 16) {
+        const int row = key_new - tt;
+        if (vrow == row % RPL) {
+          const int64_t src = (static_cast<int64_t>(b) * p.num_kv_heads + kh) * D + 8 * vch;
+          const uint4 kn = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.new_k) + src);
+          const uint4 vn = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(p.new_v) + src);
+          s_k[row * CH + (vch ^ (row % CH))] = kn;
+          *reinterpret_cast<uint4*>(s_v + ((t & 1) * 16 + row) * VRS + 16 * vch) = vn;
+          const int64_t dst = slot_new * row_stride + kh * D + 8 * vch;
+          *reinterpret_cast<uint4*>(const_cast<uint16_t*>(static_cast<const uint16_t*>(p.k)) + dst) = kn;
+          *reinterpret_cast<uint4*>(const_cast<uint16_t*>(static_cast<const uint16_t*>(p.v)) + dst) = vn;
+        }
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
@@ -430,6 +457,21 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge(DecodeParams p) {
   uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + h) * D;
   if (L == 0) {
     for (int i = threadIdx.x; i < D; i += kThreads) out[i] = 0;
+    // Fused append of a sequence with no keys to attend to: the first query
+    // head of each kv-head group writes that head's slice of the new row.
+    const int G = p.num_heads / p.num_kv_heads;
+    if (p.new_k != nullptr && h % G == 0) {
+      const int64_t slot = p.slot_mapping[b];
+      const int kh = h / G;
+      const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
+      const int64_t src = (static_cast<int64_t>(b) * p.num_kv_heads + kh) * D;
+      for (int i = threadIdx.x; slot >= 0 && i < D; i += kThreads) {
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.k))[slot * row_stride + kh * D + i] =
+            static_cast<const uint16_t*>(p.new_k)[src + i];
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.v))[slot * row_stride + kh * D + i] =
+            static_cast<const uint16_t*>(p.new_v)[src + i];
+      }
+    }
     return;
   }
   const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
@@ -616,14 +658,17 @@ extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t n
   return static_cast<size_t>(workspace_layout(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k).total);
 }
 
-extern "C" void paged_decode_attention(void* out, const void* q, const void* k_cache,
-                                       const void* v_cache, const uint32_t* cu_seqlens_k,
-                                       const int32_t* block_table, int64_t max_blocks_per_seq,
-                                       int64_t num_blocks, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                                       int64_t head_dim, int64_t page_block_size,
-                                       int64_t max_seqlen_k, int32_t window_left,
-                                       float softmax_scale, void* workspace,
-                                       size_t workspace_bytes, int dtype, void* stream) {
+namespace {
+// Shared body of both entry points; new_k / new_v / slot_mapping are null for
+// plain attention.
+void decode_attention_impl(void* out, const void* q, const void* new_k, const void* new_v,
+                           const int64_t* slot_mapping, const void* k_cache, const void* v_cache,
+                           const uint32_t* cu_seqlens_k, const int32_t* block_table,
+                           int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
+                           int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                           int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left,
+                           float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
+                           void* stream) {
   if (dtype != OXIDE_DTYPE_BF16 && dtype != OXIDE_DTYPE_F16) {
     oxide::set_error(OXIDE_ERR_UNSUPPORTED_DTYPE);
     return;
@@ -665,6 +710,9 @@ extern "C" void paged_decode_attention(void* out, const void* q, const void* k_c
   p.part_o = static_cast<float*>(workspace);
   p.part_lse = reinterpret_cast<float*>(static_cast<char*>(workspace) + wl.lse_off);
   p.out = out;
+  p.new_k = new_k;
+  p.new_v = new_v;
+  p.slot_mapping = slot_mapping;
   p.max_blocks = max_blocks_per_seq;
   p.num_blocks = static_cast<int>(num_blocks);
   p.max_seqlen_k = static_cast<int>(max_seqlen_k);
@@ -685,4 +733,47 @@ extern "C" void paged_decode_attention(void* out, const void* q, const void* k_c
     return;
   }
   oxide::check_launch();
+}
+}  // namespace
+
+extern "C" void paged_decode_attention(void* out, const void* q, const void* k_cache,
+                                       const void* v_cache, const uint32_t* cu_seqlens_k,
+                                       const int32_t* block_table, int64_t max_blocks_per_seq,
+                                       int64_t num_blocks, int64_t batch, int64_t num_heads,
+                                       int64_t num_kv_heads, int64_t head_dim,
+                                       int64_t page_block_size, int64_t max_seqlen_k,
+                                       int32_t window_left, float softmax_scale, void* workspace,
+                                       size_t workspace_bytes, int dtype, void* stream) {
+  decode_attention_impl(out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
+                        block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
+                        num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
+                        softmax_scale, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" void paged_decode_attention_append(
+    void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping,
+    void* k_cache, void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table,
+    int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch, int64_t num_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k,
+    int32_t window_left, float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
+    void* stream) {
+  if (batch > 0 && (!key || !value || !slot_mapping || !oxide::aligned16(key) ||
+                    !oxide::aligned16(value))) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  if (max_seqlen_k <= 0) {
+    // No split workgroups run: append through the plain kernel, then zeros.
+    reshape_and_cache(key, value, k_cache, v_cache, slot_mapping, batch, num_kv_heads, head_dim,
+                      dtype, stream);
+    decode_attention_impl(out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
+                          block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
+                          num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
+                          softmax_scale, workspace, workspace_bytes, dtype, stream);
+    return;
+  }
+  decode_attention_impl(out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k,
+                        block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
+                        num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
+                        softmax_scale, workspace, workspace_bytes, dtype, stream);
 }

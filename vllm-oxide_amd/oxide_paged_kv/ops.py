@@ -101,12 +101,14 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 cu_seqlens_k: torch.Tensor, block_table: torch.Tensor, max_seqlen_k: int,
                 softmax_scale: float, window_left: int | None = None,
                 page_block_size: int = 256, out: torch.Tensor | None = None,
-                workspace: torch.Tensor | None = None) -> torch.Tensor:
+                workspace: torch.Tensor | None = None, append=None) -> torch.Tensor:
     """Paged decode attention.
 
     q [B, Hq, D]; k_cache/v_cache [NB, page_block_size, Hkv, D]; cu_seqlens_k uint32-valued
     int32 tensor [B + 1] (torch has no uint32 arithmetic; the bits are passed as is);
     block_table int32 [B, max_blocks] padded with 0; window_left None = unbounded.
+    append=(key, value, slot_mapping): first append each sequence's new token (key/value
+    [B, Hkv, D], int64 slots) -- fused into the same launch (paged_decode_attention_append).
     """
     L = _lib.load()
     B, Hq, D = q.shape
@@ -123,12 +125,19 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
     max_blocks = block_table.shape[1] if block_table.dim() == 2 else 0
-    L.paged_decode_attention(
-        _ptr(out), _ptr(q), _ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k), _ptr(block_table),
-        max_blocks, NB, B, Hq, Hkv, D, BS, max_seqlen_k,
-        -1 if window_left is None else int(window_left), float(softmax_scale),
-        _ptr(workspace), workspace.numel() * workspace.element_size(), dtype_code(q.dtype),
-        _stream(q))
+    tail = (_ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k), _ptr(block_table),
+            max_blocks, NB, B, Hq, Hkv, D, BS, max_seqlen_k,
+            -1 if window_left is None else int(window_left), float(softmax_scale),
+            _ptr(workspace), workspace.numel() * workspace.element_size(), dtype_code(q.dtype),
+            _stream(q))
+    if append is None:
+        L.paged_decode_attention(_ptr(out), _ptr(q), *tail)
+    else:
+        key, value, slot_mapping = append
+        if key.shape != (B, Hkv, D) or value.shape != key.shape or slot_mapping.dtype != torch.int64:
+            raise _lib.OxideError("append needs key/value [B, Hkv, D] and int64 slot_mapping [B]")
+        L.paged_decode_attention_append(_ptr(out), _ptr(q), _ptr(key), _ptr(value),
+                                        _ptr(slot_mapping), *tail)
     _lib.check()
     return out
 
