@@ -122,18 +122,18 @@ void DecodeStep::run_layer(std::size_t layer, const void* q, const void* key, co
                            void* out, float softmax_scale, int32_t window_left,
                            hipStream_t stream) {
   if (batch_ == 0) return;
-  cache_.reshape_and_cache(layer, key, value, static_cast<const int64_t*>(d_slots_),
-                           h_slots_.size(), stream);
-  ::paged_decode_attention(out, q, cache_.k_cache(layer), cache_.v_cache(layer),
-                           static_cast<const uint32_t*>(d_cu_), static_cast<const int32_t*>(d_table_),
-                           static_cast<int64_t>(max_blocks_), static_cast<int64_t>(cache_.num_blocks()),
-                           static_cast<int64_t>(batch_), static_cast<int64_t>(num_heads_),
-                           static_cast<int64_t>(cache_.num_kv_heads()),
-                           static_cast<int64_t>(cache_.head_dim()),
-                           static_cast<int64_t>(cache_.block_size()),
-                           static_cast<int64_t>(max_seqlen_k_), window_left, softmax_scale, d_ws_,
-                           cap_ws_, cache_.dtype(), stream);
-  check_lib("paged_decode_attention");
+  // Append then attend, fused into one launch (same result as reshape_and_cache
+  // followed by paged_decode_attention).
+  ::paged_decode_attention_append(
+      out, q, key, value, static_cast<const int64_t*>(d_slots_), cache_.k_cache(layer),
+      cache_.v_cache(layer), static_cast<const uint32_t*>(d_cu_),
+      static_cast<const int32_t*>(d_table_), static_cast<int64_t>(max_blocks_),
+      static_cast<int64_t>(cache_.num_blocks()), static_cast<int64_t>(batch_),
+      static_cast<int64_t>(num_heads_), static_cast<int64_t>(cache_.num_kv_heads()),
+      static_cast<int64_t>(cache_.head_dim()), static_cast<int64_t>(cache_.block_size()),
+      static_cast<int64_t>(max_seqlen_k_), window_left, softmax_scale, d_ws_, cap_ws_,
+      cache_.dtype(), stream);
+  check_lib("paged_decode_attention_append");
 }
 
 }  // namespace oxide::host

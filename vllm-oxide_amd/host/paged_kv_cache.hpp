@@ -66,7 +66,8 @@ class DecodeStep {
   void upload(const AttnMetadata& meta, hipStream_t stream);
 
   // Layer `layer`: append key/value [B, Hkv, D], then decode attention of
-  // q [B, Hq, D] into out [B, Hq, D] (the order of models/qwen3.rs:199-208).
+  // q [B, Hq, D] into out [B, Hq, D] (the order of models/qwen3.rs:199-208),
+  // as one fused launch (paged_decode_attention_append).
   void run_layer(std::size_t layer, const void* q, const void* key, const void* value, void* out,
                  float softmax_scale, int32_t window_left, hipStream_t stream);
 
