@@ -12,8 +12,8 @@
 // to the cache dtype once.
 //
 // Pass 1 (paged_decode_split): one workgroup of 4 waves per (split, kv head,
-// sequence); a split is 512 consecutive logical keys (256 for small batches),
-// 128 per wave, walked as 16-key tiles in straight-line code with a register
+// sequence); a split is 256, 512 or 1024 consecutive logical keys
+// (choose_split_tokens), a quarter per wave, walked as 16-key tiles in straight-line code with a register
 // double buffer (tile t+1's loads are in flight while tile t computes; loads
 // past the wave's last key are clamped to a fetched tile and masked).
 //   * K and V rows are loaded as whole 256-byte head rows per 16 lanes, four
@@ -28,11 +28,14 @@
 //   its output directly, otherwise the split writes its normalised partial
 //   output o (fp32, [B, Hq, max_splits, D]) and log2-sum-exp.
 // Workgroup order is XCD-aware (decode_work_item).
-// Pass 2 (paged_decode_merge): one wave per (query head, sequence) merges the
-// splits that intersect [lo, L) with log-sum-exp weights and writes out.
+// With the fused append (paged_decode_attention_append) the workgroup whose
+// keys include position L-1 first writes its kv head's slice of the new
+// token's K/V to slot_mapping[b] and uses those values for that key.
+// Pass 2 (paged_decode_merge): 4 waves per (query head, sequence) merge the
+// splits that intersect [lo, L) with log-sum-exp weights and write out.
 //
 // Both passes read K/V exactly once; the split partials add
-// 2 * Hq * (D+1) * 4 bytes per split (under 2% at split_tokens = 512).
+// 2 * Hq * (D+1) * 4 bytes per split (under 1% at split_tokens = 1024).
 #include <math.h>
 
 #include <algorithm>
