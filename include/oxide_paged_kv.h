@@ -166,6 +166,57 @@ int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
                                             int64_t max_seqlen_k);
 
 /*
+ * Prefill attention over the paged cache.  Replaces the general (seqlen_q >= 1)
+ * call of candle_flash_attn::flash_attn_varlen_paged_windowed
+ * (crates/vllm-oxide/src/attention/flash_attn.rs:52-67) with window_right =
+ * Some(0), i.e. causal.  The prompt's K/V are appended first
+ * (reshape_and_cache with the prefill slot mapping, engine/mod.rs:186-191,
+ * models/qwen3.rs:199); keys already in the cache (a prefix hit, earlier
+ * chunks) are the first Lk - Lq keys of the sequence and need no gather.
+ *
+ *   out          [total_q, num_heads, head_dim]  written (caller-allocated)
+ *   q            [total_q, num_heads, head_dim]  rows cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1
+ *   cu_seqlens_q uint32 [batch + 1], prefix sums of query counts Lq_b
+ *                (build_prefill_metadata, attention/metadata.rs:49-80)
+ *   cu_seqlens_k uint32 [batch + 1], prefix sums of key counts Lk_b (the
+ *                whole context, new tokens included)
+ *   block_table, num_blocks, page_block_size, k_cache, v_cache: as for
+ *                paged_decode_attention
+ *   max_seqlen_q / max_seqlen_k  maxima of Lq_b / Lk_b (size the grid; larger
+ *                lengths are clamped to them)
+ *   window_left  -1 = none; w >= 0 limits query i to keys >= hi - w
+ *
+ * Masks are aligned to the bottom right, as in FlashAttention 2: query i of
+ * sequence b sees keys j with j <= hi = i + Lk_b - Lq_b (and j >= hi - w).
+ * A query that sees no key (Lk_b < Lq_b) gets zeros.  Supported: f16/bf16,
+ * head_dim 64 or 128, num_heads / num_kv_heads <= 128, any positive
+ * page_block_size.  No workspace.
+ */
+void paged_prefill_attention(void* out, const void* q, const void* k_cache, const void* v_cache,
+                             const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                             const int32_t* block_table, int64_t max_blocks_per_seq,
+                             int64_t num_blocks, int64_t batch, int64_t num_heads,
+                             int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
+                             int64_t max_seqlen_q, int64_t max_seqlen_k, int32_t window_left,
+                             float softmax_scale, int dtype, void* stream);
+
+/*
+ * The same attention over contiguous K/V.  Replaces
+ * candle_flash_attn::flash_attn_varlen(q, k, v, cu_seqlens_q, cu_seqlens_k,
+ * max_seqlen_q, max_seqlen_k, softmax_scale, causal = true) of prefill_attn,
+ * crates/vllm-oxide/src/attention/flash_attn.rs:15-37.  k / v are
+ * [total_k, num_kv_heads, head_dim]; key j of sequence b is row
+ * cu_seqlens_k[b] + j (rows >= total_k are clamped).  Other arguments and the
+ * mask as for paged_prefill_attention.
+ */
+void varlen_prefill_attention(void* out, const void* q, const void* k, const void* v,
+                              const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                              int64_t total_k, int64_t batch, int64_t num_heads,
+                              int64_t num_kv_heads, int64_t head_dim, int64_t max_seqlen_q,
+                              int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
+                              int dtype, void* stream);
+
+/*
  * Decode metadata on the device (the reference builds it on the host in every
  * layer: crates/vllm-oxide/src/engine/mod.rs:247-267, metadata.rs:20-47,
  * kv_cache_manager.rs:115-135).  From context_lens (uint32 [batch], the new

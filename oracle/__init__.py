@@ -50,6 +50,9 @@ def lib() -> ctypes.CDLL:
         L.oracle_paged_decode_attention.argtypes = [
             _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.c_float,
             ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.oracle_prefill_attention.argtypes = [
+            _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.c_float,
+            ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.oracle_xxh64.restype = ctypes.c_uint64
         L.oracle_xxh64.argtypes = [_p, ctypes.c_size_t, ctypes.c_uint64]
         _lib = L
@@ -171,6 +174,35 @@ def paged_decode_attention(q, k_cache, v_cache, cu_seqlens_k, block_table, softm
                                         _ptr(bt), bt.shape[1] if bt.ndim == 2 else 0, B, Hq, Hkv, D,
                                         BS, window_left, softmax_scale, DTYPE_CODE[dtype],
                                         int(use_f64), threads)
+    return out
+
+
+def prefill_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale: float, block_table=None,
+                      window_left: int = -1, dtype: str = "bf16", use_f64: bool = False,
+                      threads: int = 0) -> np.ndarray:
+    """Causal varlen prefill attention (attention/flash_attn.rs:15-37, and the
+    seqlen_q >= 1 call of flash_attn_varlen_paged_windowed, :52-67), masks aligned
+    bottom-right.  q [total_q, Hq, D]; k/v are the paged caches [NB, BS, Hkv, D]
+    with `block_table` [B, max_blocks], or contiguous [total_k, Hkv, D] when
+    block_table is None.  uint16 bit patterns in, fp32 [total_q, Hq, D] out."""
+    Tq, Hq, D = q.shape
+    assert q.dtype == np.uint16 and k.dtype == np.uint16 and v.dtype == np.uint16
+    if block_table is None:
+        _, Hkv, D2 = k.shape
+        BS, bt, maxb = 1, None, 0
+    else:
+        _, BS, Hkv, D2 = k.shape
+        bt = np.ascontiguousarray(block_table, dtype=np.int32)
+        maxb = bt.shape[1]
+    assert D == D2
+    cq = np.ascontiguousarray(cu_seqlens_q, dtype=np.uint32)
+    ck = np.ascontiguousarray(cu_seqlens_k, dtype=np.uint32)
+    B = len(cq) - 1
+    assert len(ck) == B + 1 and int(cq[-1]) == Tq
+    out = np.empty((Tq, Hq, D), dtype=np.float32)
+    lib().oracle_prefill_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(cq), _ptr(ck), _ptr(bt),
+                                   maxb, B, Hq, Hkv, D, BS, window_left, softmax_scale,
+                                   DTYPE_CODE[dtype], int(use_f64), threads)
     return out
 
 

@@ -16,6 +16,12 @@
  *                            contiguous K/V; closed forms (constant V, L = 1,
  *                            q = 0 -> mean V, one-hot q against orthogonal keys);
  *                            invariance under block placement; window >= L
+ *   prefill_attention        numpy fp64 masked softmax over dense score
+ *                            matrices; every query row equals a decode-oracle
+ *                            call over its causal prefix; Lq = 1 equals the
+ *                            decode oracle; the FlashAttention 2 bottom-right
+ *                            mask on a hand-worked Lq = 2, Lk = 5 case; paged
+ *                            equals contiguous; rows with no keys give zeros
  *   xxh64                    python-xxhash digests and the spec's empty-input
  *                            vector
  */
@@ -254,6 +260,104 @@ void oracle_paged_decode_attention(float* out, const uint16_t* q, const uint16_t
     free(sc);
     free(qf);
     free(acc);
+  }
+}
+
+/* Prefill attention: one query row of one head, keys [lo, hi] of sequence b.
+ * Follows attention/flash_attn.rs:15-37 (flash_attn_varlen, causal) and
+ * :52-67 (flash_attn_varlen_paged_windowed) with the FlashAttention 2 mask. */
+static int64_t prefill_key_row(const int32_t* block_table, int64_t max_blocks, int64_t block_size,
+                               const uint32_t* cu_seqlens_k, int64_t b, int64_t j) {
+  if (block_table == NULL) return (int64_t)cu_seqlens_k[b] + j;
+  return (int64_t)block_table[b * max_blocks + j / block_size] * block_size + j % block_size;
+}
+
+void oracle_prefill_attention(float* out, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                              const int32_t* block_table, int64_t max_blocks, int64_t batch,
+                              int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                              int64_t block_size, int32_t window_left, float softmax_scale,
+                              int dtype, int use_f64, int threads) {
+  const int64_t group = num_heads / num_kv_heads;
+  const int64_t row_stride = num_kv_heads * head_dim;
+  const int64_t total_q = (int64_t)cu_seqlens_q[batch];
+  const int nthreads = threads > 0 ? threads : omp_get_max_threads();
+#pragma omp parallel num_threads(nthreads)
+  {
+    int64_t cap = 0;
+    double* sc = NULL;
+    float* qf = (float*)malloc(sizeof(float) * (size_t)head_dim);
+    double* acc = (double*)malloc(sizeof(double) * (size_t)head_dim);
+    float* accf = (float*)malloc(sizeof(float) * (size_t)head_dim);
+#pragma omp for schedule(dynamic, 4)
+    for (int64_t tq = 0; tq < total_q * num_heads; ++tq) {
+      const int64_t t = tq / num_heads, h = tq % num_heads, kh = h / group;
+      int64_t b = 0;
+      while (b + 1 < batch && (int64_t)cu_seqlens_q[b + 1] <= t) ++b;
+      const int64_t Lq = (int64_t)cu_seqlens_q[b + 1] - (int64_t)cu_seqlens_q[b];
+      const int64_t Lk = (int64_t)cu_seqlens_k[b + 1] - (int64_t)cu_seqlens_k[b];
+      const int64_t i = t - (int64_t)cu_seqlens_q[b];
+      int64_t hi = i + Lk - Lq;
+      if (hi > Lk - 1) hi = Lk - 1;
+      int64_t lo = window_left < 0 ? 0 : i + Lk - Lq - window_left;
+      if (lo < 0) lo = 0;
+      const int64_t n = hi >= lo ? hi - lo + 1 : 0;
+      float* o = out + tq * head_dim;
+      if (n == 0) {
+        for (int64_t d = 0; d < head_dim; ++d) o[d] = 0.f;
+        continue;
+      }
+      if (n > cap) {
+        free(sc);
+        cap = n;
+        sc = (double*)malloc(sizeof(double) * (size_t)cap);
+      }
+      for (int64_t d = 0; d < head_dim; ++d) qf[d] = oracle_half_to_float(q[tq * head_dim + d], dtype);
+      double mx = -INFINITY;
+      for (int64_t x = 0; x < n; ++x) {
+        const uint16_t* kr = k + prefill_key_row(block_table, max_blocks, block_size, cu_seqlens_k, b,
+                                                 lo + x) * row_stride + kh * head_dim;
+        double s;
+        if (use_f64) {
+          double dot = 0.0;
+          for (int64_t d = 0; d < head_dim; ++d) dot += (double)qf[d] * (double)oracle_half_to_float(kr[d], dtype);
+          s = dot * (double)softmax_scale;
+        } else {
+          float dot = 0.f;
+          for (int64_t d = 0; d < head_dim; ++d) dot += qf[d] * oracle_half_to_float(kr[d], dtype);
+          s = (double)(dot * softmax_scale);
+        }
+        sc[x] = s;
+        if (s > mx) mx = s;
+      }
+      if (use_f64) {
+        double l = 0.0;
+        for (int64_t d = 0; d < head_dim; ++d) acc[d] = 0.0;
+        for (int64_t x = 0; x < n; ++x) {
+          const uint16_t* vr = v + prefill_key_row(block_table, max_blocks, block_size, cu_seqlens_k, b,
+                                                   lo + x) * row_stride + kh * head_dim;
+          const double p = exp(sc[x] - mx);
+          l += p;
+          for (int64_t d = 0; d < head_dim; ++d) acc[d] += p * (double)oracle_half_to_float(vr[d], dtype);
+        }
+        for (int64_t d = 0; d < head_dim; ++d) o[d] = (float)(acc[d] / l);
+      } else {
+        float l = 0.f;
+        for (int64_t d = 0; d < head_dim; ++d) accf[d] = 0.f;
+        for (int64_t x = 0; x < n; ++x) {
+          const uint16_t* vr = v + prefill_key_row(block_table, max_blocks, block_size, cu_seqlens_k, b,
+                                                   lo + x) * row_stride + kh * head_dim;
+          const float p = expf((float)sc[x] - (float)mx);
+          l += p;
+          for (int64_t d = 0; d < head_dim; ++d) accf[d] += p * oracle_half_to_float(vr[d], dtype);
+        }
+        for (int64_t d = 0; d < head_dim; ++d) o[d] = accf[d] / l;
+      }
+    }
+    free(sc);
+    free(qf);
+    free(acc);
+    free(accf);
   }
 }
 

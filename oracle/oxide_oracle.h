@@ -72,6 +72,26 @@ void oracle_paged_decode_attention(float* out, const uint16_t* q, const uint16_t
                                    int64_t block_size, int32_t window_left, float softmax_scale,
                                    int dtype, int use_f64, int threads);
 
+/* Prefill attention: the general (seqlen_q >= 1) call of
+ * flash_attn_varlen_paged_windowed with window_right = 0 (causal), and, with
+ * block_table == NULL, flash_attn_varlen(..., causal = true) over contiguous
+ * K/V (attention/flash_attn.rs:15-37).  Sequence b has Lq = cu_seqlens_q[b+1] -
+ * cu_seqlens_q[b] queries (rows cu_seqlens_q[b] + i of q [total_q, Hq, D]) and
+ * Lk = cu_seqlens_k[b+1] - cu_seqlens_k[b] keys.  Causal masks are aligned to
+ * the bottom right, as in FlashAttention 2 for Lq != Lk: query i sees keys
+ *   j <= hi = i + Lk - Lq   and, when window_left >= 0, j >= hi - window_left
+ * (and 0 <= j < Lk).  A query with no visible key gives zeros.  Key j lives at
+ * cache row block_table[b * max_blocks + j / block_size] * block_size +
+ * j % block_size of [num_blocks, block_size, Hkv, D] (paged), or at row
+ * cu_seqlens_k[b] + j of [total_k, Hkv, D] (block_table == NULL).  fp32 `out`
+ * [total_q, Hq, D]; arithmetic as in oracle_paged_decode_attention. */
+void oracle_prefill_attention(float* out, const uint16_t* q, const uint16_t* k, const uint16_t* v,
+                              const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                              const int32_t* block_table, int64_t max_blocks, int64_t batch,
+                              int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                              int64_t block_size, int32_t window_left, float softmax_scale,
+                              int dtype, int use_f64, int threads);
+
 /* XXH64 (public xxHash spec, 64-bit variant) of `len` bytes with `seed`. */
 uint64_t oracle_xxh64(const void* data, size_t len, uint64_t seed);
 

@@ -212,6 +212,107 @@ def test_attention_window_edge_counts_w_plus_one_keys():
     np.testing.assert_allclose(out[0, 0], want, atol=1e-6)
 
 
+# ------------------------------------------------------------------ prefill
+def _prefill_case(seed, lq, lk, Hq, Hkv, D, BS, NB, dtype="bf16"):
+    rng = np.random.default_rng(seed)
+    _, kc, vc, cuk, table = _rand_case(seed, len(lk), Hq, Hkv, D, BS, NB, lk, dtype)
+    cuq = np.zeros(len(lq) + 1, np.uint32)
+    cuq[1:] = np.cumsum(lq)
+    q = normal_bits(rng, (int(cuq[-1]), Hq, D), dtype)
+    return q, kc, vc, cuq, cuk, table
+
+
+def _numpy_f64_prefill(q, kc, vc, cuq, cuk, table, scale, window, dtype):
+    """Independent dense routine: gather K/V, full [Lq, Lk] score matrix, boolean
+    mask from the FlashAttention 2 bottom-right rule, masked softmax in float64."""
+    Tq, Hq, D = q.shape
+    NB, BS, Hkv, _ = kc.shape
+    G = Hq // Hkv
+    qf = oracle.bits_to_f32(q, dtype).astype(np.float64)
+    kf = oracle.bits_to_f32(kc, dtype).astype(np.float64).reshape(-1, Hkv, D)
+    vf = oracle.bits_to_f32(vc, dtype).astype(np.float64).reshape(-1, Hkv, D)
+    out = np.zeros((Tq, Hq, D))
+    for b in range(len(cuq) - 1):
+        q0, Lq = int(cuq[b]), int(cuq[b + 1] - cuq[b])
+        Lk = int(cuk[b + 1] - cuk[b])
+        if Lq == 0 or Lk == 0:
+            continue
+        j = np.arange(Lk)
+        rows = table[b, j // BS].astype(np.int64) * BS + j % BS
+        ii, jj = np.meshgrid(np.arange(Lq), j, indexing="ij")
+        mask = jj <= ii + Lk - Lq
+        if window >= 0:
+            mask &= jj >= ii + Lk - Lq - window
+        for h in range(Hq):
+            s = qf[q0:q0 + Lq, h] @ kf[rows, h // G].T * scale
+            s = np.where(mask, s, -np.inf)
+            m = s.max(axis=1, keepdims=True)
+            m = np.where(np.isfinite(m), m, 0.0)
+            p = np.exp(s - m)
+            den = p.sum(axis=1, keepdims=True)
+            o = (p @ vf[rows, h // G]) / np.where(den > 0, den, 1.0)
+            out[q0:q0 + Lq, h] = o
+    return out
+
+
+@pytest.mark.parametrize("G,D,BS,window,dtype", [(4, 128, 256, -1, "bf16"), (2, 64, 16, 23, "bf16"),
+                                                 (1, 128, 32, -1, "f16"), (8, 64, 64, 100, "f16")])
+def test_prefill_matches_numpy_f64(G, D, BS, window, dtype):
+    Hkv = 2
+    # prompt without prefix, prompt after a cached prefix, Lk < Lq, empty query list
+    lq, lk = [37, 20, 9, 0], [37, 150, 4, 30]
+    q, kc, vc, cuq, cuk, table = _prefill_case(11, lq, lk, G * Hkv, Hkv, D, BS, 40, dtype)
+    scale = 1 / math.sqrt(D)
+    want = _numpy_f64_prefill(q, kc, vc, cuq, cuk, table, scale, window, dtype)
+    got64 = oracle.prefill_attention(q, kc, vc, cuq, cuk, scale, table, window, dtype, use_f64=True)
+    got32 = oracle.prefill_attention(q, kc, vc, cuq, cuk, scale, table, window, dtype)
+    np.testing.assert_allclose(got64, want, atol=1e-7, rtol=1e-6)
+    np.testing.assert_allclose(got32, want, atol=2e-5, rtol=1e-4)
+    # Lq = 9 with Lk = 4: queries 0..4 see no key (hi < 0) and are zero.
+    assert np.all(got64[57:62] == 0) and np.any(got64[62] != 0)
+
+
+def test_prefill_rows_equal_decode_over_their_prefix():
+    """Query i of a sequence is a decode call whose context is keys [0, i + Lk - Lq]."""
+    lq, lk = [12, 7], [12, 300]
+    q, kc, vc, cuq, cuk, table = _prefill_case(12, lq, lk, 8, 2, 64, 16, 40)
+    for window in (-1, 5):
+        got = oracle.prefill_attention(q, kc, vc, cuq, cuk, 0.2, table, window)
+        for b in range(2):
+            for i in range(lq[b]):
+                L = i + lk[b] - lq[b] + 1
+                t = int(cuq[b]) + i
+                dec = oracle.paged_decode_attention(q[t][None], kc, vc, np.array([0, L], np.uint32),
+                                                    table[b][None], 0.2, window)
+                assert np.array_equal(got[t], dec[0]), (b, i, window)
+
+
+def test_prefill_fa2_bottom_right_mask_hand_case():
+    """Lq = 2, Lk = 5, q = 0 (uniform weights): query 0 averages keys 0..3 and
+    query 1 keys 0..4; with window_left = 1, keys 2..3 and 3..4."""
+    q, kc, vc, cuq, cuk, table = _prefill_case(13, [2], [5], 1, 1, 64, 16, 4)
+    qz = np.zeros_like(q)
+    V = oracle.bits_to_f32(vc[table[0, 0], :5, 0], "bf16").astype(np.float64)
+    out = oracle.prefill_attention(qz, kc, vc, cuq, cuk, 1.0, table, -1, use_f64=True)
+    np.testing.assert_allclose(out[0, 0], V[:4].mean(0), atol=1e-6)
+    np.testing.assert_allclose(out[1, 0], V[:5].mean(0), atol=1e-6)
+    out = oracle.prefill_attention(qz, kc, vc, cuq, cuk, 1.0, table, 1, use_f64=True)
+    np.testing.assert_allclose(out[0, 0], V[2:4].mean(0), atol=1e-6)
+    np.testing.assert_allclose(out[1, 0], V[3:5].mean(0), atol=1e-6)
+
+
+def test_prefill_contiguous_equals_paged():
+    lq, lk = [20, 33], [50, 33]
+    q, kc, vc, cuq, cuk, table = _prefill_case(14, lq, lk, 4, 2, 64, 16, 20)
+    rows = np.concatenate([table[b, np.arange(lk[b]) // 16].astype(np.int64) * 16 + np.arange(lk[b]) % 16
+                           for b in range(2)])
+    kcont = kc.reshape(-1, 2, 64)[rows]
+    vcont = vc.reshape(-1, 2, 64)[rows]
+    paged = oracle.prefill_attention(q, kc, vc, cuq, cuk, 0.3, table, 7)
+    cont = oracle.prefill_attention(q, kcont, vcont, cuq, cuk, 0.3, None, 7)
+    assert np.array_equal(paged, cont)
+
+
 # ------------------------------------------------------------------- xxh64
 def test_xxh64_matches_python_xxhash():
     import xxhash

@@ -1,0 +1,63 @@
+// gfx950 (CDNA4) tile helpers shared by the attention kernels: the
+// 16x16x32 bf16/f16 matrix-core op, fp32 -> 16-bit rounding and the
+// transposing LDS read.
+//
+// v_mfma_f32_16x16x32_{bf16,f16} operand layout (lane l, g = l / 16):
+//   A[16 x 32]: lane l holds A[l % 16][8g .. 8g+7]
+//   B[32 x 16]: lane l holds B[8g .. 8g+7][l % 16]
+//   C[16 x 16]: lane l holds C[4g + j][l % 16], j = 0..3
+// ds_read_b64_tr_b16 (lds_read_tr16): within each 16-lane group, lane i
+// receives element (i % 4) of the 8-byte reads of lanes 4j + i/4, j = 0..3;
+// reading row 4g + i/4, columns c0 + 4(i % 4) .. +3 of a row-major 16-bit
+// tile therefore hands lane i the column c0 + i of rows 4g .. 4g+3.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+struct Bf16Tag {};
+struct F16Tag {};
+
+__device__ __forceinline__ floatx4 mfma16x16x32(Bf16Tag, uint4 a, uint4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx4 mfma16x16x32(F16Tag, uint4 a, uint4 b, floatx4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// fp32 -> 16-bit storage, round to nearest even.
+__device__ __forceinline__ uint16_t pack1(Bf16Tag, float f) {
+  const uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // NaN
+  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+__device__ __forceinline__ uint16_t pack1(F16Tag, float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+
+typedef short v4i16_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
+
+__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
+  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16_t*)((__attribute__((address_space(3))) char*)(p)));
+  return __builtin_bit_cast(uint2, r);
+}
+
+// Two fp32 probabilities -> packed 16-bit pair of the MFMA input type.
+__device__ __forceinline__ uint32_t pack2(Bf16Tag, float lo, float hi) {
+  return static_cast<uint32_t>(pack1(Bf16Tag{}, lo)) | (static_cast<uint32_t>(pack1(Bf16Tag{}, hi)) << 16);
+}
+__device__ __forceinline__ uint32_t pack2(F16Tag, float lo, float hi) {
+  return static_cast<uint32_t>(pack1(F16Tag{}, lo)) | (static_cast<uint32_t>(pack1(F16Tag{}, hi)) << 16);
+}
+
+}  // namespace

@@ -40,13 +40,11 @@
 
 #include <algorithm>
 
+#include "cdna4_tile.hpp"
 #include "oxide_common.hpp"
 
 namespace {
 
-typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
-typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 // Build-time tuning knobs (defaults are the tuned values).
 #ifndef OXIDE_SPLIT_TOKENS
@@ -77,27 +75,6 @@ __device__ __forceinline__ uint4 load_kv16(const uint16_t* p) {
 #endif
 }
 
-struct Bf16Tag {};
-struct F16Tag {};
-
-__device__ __forceinline__ floatx4 mfma16x16x32(Bf16Tag, uint4 a, uint4 b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
-}
-__device__ __forceinline__ floatx4 mfma16x16x32(F16Tag, uint4 a, uint4 b, floatx4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
-                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
-}
-
-// fp32 -> 16-bit storage, round to nearest even.
-__device__ __forceinline__ uint16_t pack1(Bf16Tag, float f) {
-  const uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);  // NaN
-  return static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-}
-__device__ __forceinline__ uint16_t pack1(F16Tag, float f) {
-  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
-}
 
 struct DecodeParams {
   const void* q;
@@ -191,22 +168,6 @@ __device__ __forceinline__ bool decode_work_item(const DecodeParams& p, int& spl
 //   * 32 fp32 accumulators per lane for D = 128, whatever the group size.
 // V rows in LDS are padded to D*2 + 32 bytes so the 4 rows one 16-lane group
 // reads land on disjoint banks.
-typedef short v4i16_t __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4i16_t lds_v4i16_t;
-
-__device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
-  const v4i16_t r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (lds_v4i16_t*)((__attribute__((address_space(3))) char*)(p)));
-  return __builtin_bit_cast(uint2, r);
-}
-
-// Two fp32 probabilities -> packed 16-bit pair of the MFMA input type.
-__device__ __forceinline__ uint32_t pack2(Bf16Tag, float lo, float hi) {
-  return static_cast<uint32_t>(pack1(Bf16Tag{}, lo)) | (static_cast<uint32_t>(pack1(Bf16Tag{}, hi)) << 16);
-}
-__device__ __forceinline__ uint32_t pack2(F16Tag, float lo, float hi) {
-  return static_cast<uint32_t>(pack1(F16Tag{}, lo)) | (static_cast<uint32_t>(pack1(F16Tag{}, hi)) << 16);
-}
 
 template <class Tag, int D, int G, int TILES>
 __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_split(DecodeParams p) {

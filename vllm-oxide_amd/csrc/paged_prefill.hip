@@ -1,0 +1,438 @@
+// Prefill attention over the paged KV cache (and over contiguous K/V), causal
+// with an optional left window and GQA, for gfx950.
+//
+// What it computes: the seqlen_q >= 1 call of flash_attn_varlen_paged_windowed
+// (crates/vllm-oxide/src/attention/flash_attn.rs:52-67) with window_right = 0,
+// and, over contiguous K/V, flash_attn_varlen(..., causal = true)
+// (flash_attn.rs:15-37, called from the prefill branch of qwen3.rs).  Sequence
+// b has Lq = cu_seqlens_q[b+1] - cu_seqlens_q[b] query tokens and
+// Lk = cu_seqlens_k[b+1] - cu_seqlens_k[b] keys; the masks are aligned to the
+// bottom right (FlashAttention 2): query i, head h sees keys
+//     j <= hi = i + Lk - Lq,   j >= hi - window_left (window_left >= 0 only),
+// of kv head h / G.  Keys already in the cache before this step (a prefix
+// hit, or earlier chunks of a chunked prefill) are simply the first Lk - Lq
+// keys, so the paged form needs no gather.  A query with no visible key gets
+// zeros.  fp32 accumulation, output rounded to the input dtype once.
+//
+// Work split: one workgroup of 4 waves per (128 (token, head) rows of one kv
+// head's group, kv head, sequence).  Row r of the workgroup is token r / G,
+// head r % G of the group, so the G heads that share a kv head share every
+// K/V tile.  Each wave owns 32 rows = two 16-column blocks of the MFMA tiles.
+// K/V advance in 64-key tiles staged through LDS by the whole workgroup with a
+// register prefetch of the next tile and two LDS buffers (one barrier per
+// tile).  Per tile and wave:
+//   * S^T[key][row] = K . Q^T on the matrix cores: A = 16 keys x 32 d from the
+//     K tile (XOR-swizzled 16-byte chunks), B = the rows' queries, held in
+//     registers for the whole kernel.  Lane l gets keys 4(l/16)+j of row l%16.
+//   * online softmax per row in the log2 domain; a row's keys sit in the 4
+//     lane groups of its column, so maxima take two shuffles (xor 16, 32) and
+//     the sums stay per lane until the end.
+//   * O^T[d][row] += V^T . P^T: A = V^T read from the row-major V tile with
+//     the transposing LDS read (keys 4g..4g+3 and 16+4g..16+4g+3 of a 32-key
+//     step), B = the lane's own probabilities in the same key order, so P
+//     never moves between lanes.  Every accumulator of a lane belongs to its
+//     own row: rescaling is a per-lane multiply.
+// Workgroup order is XCD-aware: all row tiles of one (sequence, kv head) run
+// on one XCD (workgroup i runs on XCD i % 8), so its K/V is fetched from HBM
+// once into that XCD's L2 and re-read from there; within a unit the tiles
+// with the most keys (last tokens) start first.
+#include <math.h>
+
+#include <algorithm>
+
+#include "cdna4_tile.hpp"
+#include "oxide_common.hpp"
+
+namespace {
+
+constexpr int kPfWaves = 4;
+constexpr int kPfThreads = 64 * kPfWaves;
+constexpr int kPfRows = kPfWaves * 32;  // (token, head) rows per workgroup
+constexpr int kPfKeys = 64;             // keys per K/V tile
+constexpr int kPfXcds = 8;
+
+struct PrefillParams {
+  const void* q;    // [total_q, Hq, D]
+  const void* k;    // paged [NB, BS, Hkv, D] or contiguous [total_k, Hkv, D]
+  const void* v;
+  void* out;        // [total_q, Hq, D]
+  const uint32_t* cu_seqlens_q;
+  const uint32_t* cu_seqlens_k;
+  const int32_t* block_table;  // null: contiguous K/V, key j of b at row cu_seqlens_k[b] + j
+  int64_t max_blocks;
+  int64_t num_rows;            // rows of the K/V view (clamp for bad indices)
+  int num_blocks;
+  int max_seqlen_q;
+  int max_seqlen_k;
+  int num_heads;
+  int num_kv_heads;
+  int group;
+  int tokens_per_wg;
+  int tiles_per_unit;
+  int units;                   // batch * num_kv_heads
+  int block_size;
+  int window_left;
+  float scale_log2;
+};
+
+__device__ __forceinline__ int clamp_len(int64_t n, int cap) {
+  return static_cast<int>(n < 0 ? 0 : (n > cap ? cap : n));
+}
+
+template <class Tag, int D>
+__global__ __launch_bounds__(kPfThreads) void paged_prefill_attn(PrefillParams p) {
+  constexpr int CH = D / 8;                  // 16-byte chunks per head row
+  constexpr int KK = D / 32;                 // MFMA k-steps of Q.K
+  constexpr int NDB = D / 16;                // 16-wide d blocks of the output
+  constexpr int VRS = 2 * D + 32;            // padded V row in LDS (bytes)
+  constexpr int KT_BYTES = kPfKeys * D * 2;
+  constexpr int BUF = KT_BYTES + kPfKeys * VRS;
+  constexpr int RPI = kPfThreads / CH;       // tile rows per load instruction
+  constexpr int NLD = kPfKeys / RPI;         // load instructions per tensor and tile
+  static_assert(kPfKeys % RPI == 0, "tile rows");
+  __shared__ __align__(16) char smem[2 * BUF];
+
+  // XCD-aware work item: unit (sequence, kv head) u sits on XCD u % 8 and its
+  // tiles are consecutive workgroups there, heaviest first.
+  const int i = blockIdx.x;
+  const int j = i / kPfXcds;
+  const int u = (j / p.tiles_per_unit) * kPfXcds + i % kPfXcds;
+  if (u >= p.units) return;
+  const int tile = p.tiles_per_unit - 1 - j % p.tiles_per_unit;
+  const int b = u / p.num_kv_heads;
+  const int kh = u % p.num_kv_heads;
+
+  const int Lq = clamp_len(static_cast<int64_t>(p.cu_seqlens_q[b + 1]) - p.cu_seqlens_q[b], p.max_seqlen_q);
+  const int Lk = clamp_len(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - p.cu_seqlens_k[b], p.max_seqlen_k);
+  const int t0 = tile * p.tokens_per_wg;
+  if (t0 >= Lq) return;
+  const int t1 = min(Lq, t0 + p.tokens_per_wg);
+  const int off = Lk - Lq;  // hi of token t is t + off
+  const int G = p.group;
+  const int W = p.window_left;
+
+  // Key range of the workgroup: [klo, khi] (empty when khi < klo).
+  const int khi = min(Lk - 1, t1 - 1 + off);
+  const int klo = W >= 0 ? max(0, t0 + off - W) : 0;
+  const int kt0 = klo & ~(kPfKeys - 1);
+  const int ntiles = khi >= klo ? (khi - kt0) / kPfKeys + 1 : 0;
+
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int grp = lane >> 4;
+  const int64_t q0 = p.cu_seqlens_q[b];
+  const int rows_used = p.tokens_per_wg * G;
+
+  // This lane's two rows (columns of the MFMA tiles): token, head, key range.
+  int hi_r[2], lo_r[2];
+  int64_t qrow[2];
+  bool valid[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int r = wave * 32 + c * 16 + r16;
+    const int t = t0 + r / G;
+    valid[c] = r < rows_used && t < t1;
+    qrow[c] = valid[c] ? (q0 + t) * p.num_heads + kh * G + r % G : 0;
+    hi_r[c] = valid[c] ? t + off : -1;
+    lo_r[c] = valid[c] && W >= 0 ? t + off - W : 0;
+  }
+  // Key range of the wave's valid rows (wave-uniform) for skipping tiles.
+  const int wr0 = wave * 32;
+  const int wt_first = t0 + wr0 / G;
+  const int wt_last = min(t1 - 1, t0 + min(wr0 + 31, rows_used - 1) / G);
+  const bool wave_active = wr0 < rows_used && wt_first < t1;
+  const int wave_hi = min(Lk - 1, wt_last + off);
+  const int wave_lo = W >= 0 ? wt_first + off - W : 0;
+
+  uint4 qb[2][KK];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qrow[c] * D;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk)
+      qb[c][kk] = valid[c] ? *reinterpret_cast<const uint4*>(qp + 8 * (grp + 4 * kk)) : make_uint4(0, 0, 0, 0);
+  }
+
+  // Tile loads: lane -> (row, chunk) of the 64-key tile; keys past Lk - 1 read
+  // row Lk - 1 (finite data, masked in the scores).
+  const int ldch = threadIdx.x % CH;
+  const int ldrow = threadIdx.x / CH;
+  const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + kh * D + 8 * ldch;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + kh * D + 8 * ldch;
+  const int32_t* bt = p.block_table ? p.block_table + b * p.max_blocks : nullptr;
+  const int64_t kstart = p.cu_seqlens_k[b];
+  const bool paged = bt != nullptr;
+  uint4 kr[NLD], vr[NLD];
+#define OXIDE_PF_LOAD_TILE(KB0)                                                              \
+  _Pragma("unroll") for (int x = 0; x < NLD; ++x) {                                          \
+    const int key = min((KB0) + ldrow + RPI * x, Lk - 1);                                    \
+    const int blk = paged ? min(max(bt[key / p.block_size], 0), p.num_blocks - 1) : 0;       \
+    const int64_t row = paged ? static_cast<int64_t>(blk) * p.block_size + key % p.block_size \
+                              : min(kstart + key, p.num_rows - 1);                           \
+    kr[x] = *reinterpret_cast<const uint4*>(kbase + row * row_stride);                       \
+    vr[x] = *reinterpret_cast<const uint4*>(vbase + row * row_stride);                       \
+  }
+#define OXIDE_PF_STORE_TILE(BUFI)                                                            \
+  _Pragma("unroll") for (int x = 0; x < NLD; ++x) {                                          \
+    const int row = ldrow + RPI * x;                                                         \
+    reinterpret_cast<uint4*>(smem + (BUFI) * BUF)[row * CH + (ldch ^ (row % CH))] = kr[x];   \
+    *reinterpret_cast<uint4*>(smem + (BUFI) * BUF + KT_BYTES + row * VRS + 16 * ldch) = vr[x]; \
+  }
+
+  float m_r[2] = {-INFINITY, -INFINITY};
+  float l_r[2] = {0.f, 0.f};
+  floatx4 acc[2][NDB];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) acc[c][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  if (ntiles > 0) {
+    OXIDE_PF_LOAD_TILE(kt0)
+    OXIDE_PF_STORE_TILE(0)
+  }
+  __syncthreads();
+  for (int it = 0; it < ntiles; ++it) {
+    const int kb0 = kt0 + it * kPfKeys;
+    const bool more = it + 1 < ntiles;
+    // The next tile, or (last iteration) this tile again from L2: an
+    // unconditional load keeps kr / vr in registers.
+    OXIDE_PF_LOAD_TILE(more ? kb0 + kPfKeys : kb0)
+    if (wave_active && kb0 <= wave_hi && kb0 + kPfKeys - 1 >= wave_lo) {
+      const uint4* sk = reinterpret_cast<const uint4*>(smem + (it & 1) * BUF);
+      const char* sv = smem + (it & 1) * BUF + KT_BYTES;
+
+      // Scores of 4 key blocks x 2 row blocks.
+      floatx4 sc[2][4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        sc[0][kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+        sc[1][kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) {
+          const uint4 ka = sk[(kb * 16 + r16) * CH + ((grp + 4 * kk) ^ (r16 % CH))];
+          sc[0][kb] = mfma16x16x32(Tag{}, ka, qb[0][kk], sc[0][kb]);
+          sc[1][kb] = mfma16x16x32(Tag{}, ka, qb[1][kk], sc[1][kb]);
+        }
+      }
+
+      // Mask only where the tile crosses some row's key range.
+      bool lane_mask = false;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) lane_mask |= !(kb0 >= lo_r[c] && kb0 + kPfKeys - 1 <= hi_r[c]);
+      const bool need_mask = __ballot(lane_mask) != 0;
+
+      uint4 pb[2][2];
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float x[4][4];
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float s = sc[c][kb][e] * p.scale_log2;
+            if (need_mask) {
+              const int key = kb0 + kb * 16 + 4 * grp + e;
+              if (key > hi_r[c] || key < lo_r[c]) s = -INFINITY;
+            }
+            x[kb][e] = s;
+            mt = fmaxf(mt, s);
+          }
+        mt = fmaxf(mt, __shfl_xor(mt, 16));
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mnew = fmaxf(m_r[c], mt);
+        const float msafe = mnew == -INFINITY ? 0.f : mnew;
+        const float alpha = __builtin_amdgcn_exp2f(m_r[c] - msafe);
+        float psum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[kb][e] = __builtin_amdgcn_exp2f(x[kb][e] - msafe);
+            psum += x[kb][e];
+          }
+        l_r[c] = l_r[c] * alpha + psum;
+        m_r[c] = mnew;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) acc[c][db] *= alpha;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2) {
+          pb[c][s2].x = pack2(Tag{}, x[2 * s2][0], x[2 * s2][1]);
+          pb[c][s2].y = pack2(Tag{}, x[2 * s2][2], x[2 * s2][3]);
+          pb[c][s2].z = pack2(Tag{}, x[2 * s2 + 1][0], x[2 * s2 + 1][1]);
+          pb[c][s2].w = pack2(Tag{}, x[2 * s2 + 1][2], x[2 * s2 + 1][3]);
+        }
+      }
+
+      // O^T += V^T . P^T over two 32-key steps.
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const char* vlo = sv + (32 * s2 + 4 * grp + r16 / 4) * VRS + 8 * (r16 % 4);
+        const char* vhi = vlo + 16 * VRS;
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) {
+          const uint2 a0 = lds_read_tr16(vlo + 32 * db);
+          const uint2 a1 = lds_read_tr16(vhi + 32 * db);
+          const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
+          acc[0][db] = mfma16x16x32(Tag{}, va, pb[0][s2], acc[0][db]);
+          acc[1][db] = mfma16x16x32(Tag{}, va, pb[1][s2], acc[1][db]);
+        }
+      }
+    }
+    if (more) {
+      OXIDE_PF_STORE_TILE((it + 1) & 1)
+    }
+    __syncthreads();
+  }
+
+  // Row totals (the 4 lane groups of a column hold disjoint keys), then
+  // out[row][d] for d = 16 db + 4 grp + e.
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    float l = l_r[c];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    if (!valid[c]) continue;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    uint16_t* op = static_cast<uint16_t*>(p.out) + qrow[c] * D + 4 * grp;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) {
+      uint2 w;
+      w.x = pack2(Tag{}, acc[c][db][0] * inv, acc[c][db][1] * inv);
+      w.y = pack2(Tag{}, acc[c][db][2] * inv, acc[c][db][3] * inv);
+      *reinterpret_cast<uint2*>(op + 16 * db) = w;
+    }
+  }
+#undef OXIDE_PF_LOAD_TILE
+#undef OXIDE_PF_STORE_TILE
+}
+
+int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+template <class Tag>
+bool launch_prefill(const PrefillParams& p, int head_dim, hipStream_t s) {
+  const int64_t units8 = ceil_div64(p.units, kPfXcds) * kPfXcds;
+  const dim3 grid(static_cast<unsigned>(units8 * p.tiles_per_unit));
+  if (head_dim == 128) {
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, 128>), grid, dim3(kPfThreads), 0, s, p);
+    return true;
+  }
+  if (head_dim == 64) {
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, 64>), grid, dim3(kPfThreads), 0, s, p);
+    return true;
+  }
+  return false;
+}
+
+void prefill_impl(void* out, const void* q, const void* k, const void* v, const uint32_t* cu_seqlens_q,
+                  const uint32_t* cu_seqlens_k, const int32_t* block_table, int64_t max_blocks_per_seq,
+                  int64_t num_blocks, int64_t num_rows, int64_t batch, int64_t num_heads,
+                  int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
+                  int64_t max_seqlen_q, int64_t max_seqlen_k, int32_t window_left,
+                  float softmax_scale, int dtype, void* stream) {
+  if (dtype != OXIDE_DTYPE_BF16 && dtype != OXIDE_DTYPE_F16) {
+    oxide::set_error(OXIDE_ERR_UNSUPPORTED_DTYPE);
+    return;
+  }
+  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+      max_seqlen_q < 0 || max_seqlen_k < 0 || batch > 65535 || num_heads > 65535 ||
+      max_seqlen_q > INT32_MAX / 2 || max_seqlen_k > INT32_MAX / 2) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  if (batch == 0 || max_seqlen_q == 0) return;
+  if (!out || !q || !cu_seqlens_q || !cu_seqlens_k || !oxide::aligned16(out) || !oxide::aligned16(q)) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  if (max_seqlen_k > 0) {
+    if (!k || !v || !oxide::aligned16(k) || !oxide::aligned16(v)) {
+      oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+      return;
+    }
+    if (block_table != nullptr) {
+      if (page_block_size <= 0 || num_blocks <= 0 || num_blocks > INT32_MAX || max_blocks_per_seq < 0 ||
+          page_block_size > INT32_MAX || max_blocks_per_seq * page_block_size < max_seqlen_k) {
+        oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+        return;
+      }
+    } else if (num_rows <= 0) {
+      oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+      return;
+    }
+  }
+  const int64_t group = num_heads / num_kv_heads;
+  if ((head_dim != 64 && head_dim != 128) || group > kPfRows) {
+    oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
+    return;
+  }
+  PrefillParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.out = out;
+  p.cu_seqlens_q = cu_seqlens_q;
+  p.cu_seqlens_k = cu_seqlens_k;
+  p.block_table = block_table;
+  p.max_blocks = max_blocks_per_seq;
+  p.num_rows = block_table ? num_blocks * page_block_size : num_rows;
+  p.num_blocks = static_cast<int>(block_table ? num_blocks : 0);
+  p.max_seqlen_q = static_cast<int>(max_seqlen_q);
+  p.max_seqlen_k = static_cast<int>(max_seqlen_k);
+  p.num_heads = static_cast<int>(num_heads);
+  p.num_kv_heads = static_cast<int>(num_kv_heads);
+  p.group = static_cast<int>(group);
+  p.tokens_per_wg = static_cast<int>(kPfRows / group);
+  const int64_t tiles = ceil_div64(max_seqlen_q, p.tokens_per_wg);
+  const int64_t units = batch * num_kv_heads;
+  if (units > INT32_MAX / 2 || ceil_div64(units, kPfXcds) * kPfXcds * tiles > INT32_MAX) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  p.tiles_per_unit = static_cast<int>(tiles);
+  p.units = static_cast<int>(units);
+  p.block_size = static_cast<int>(block_table ? page_block_size : 1);
+  p.window_left = window_left < 0 ? -1 : window_left;
+  p.scale_log2 = softmax_scale * 1.4426950408889634f;
+  hipStream_t s = oxide::as_stream(stream);
+  const bool ok = dtype == OXIDE_DTYPE_BF16 ? launch_prefill<Bf16Tag>(p, static_cast<int>(head_dim), s)
+                                            : launch_prefill<F16Tag>(p, static_cast<int>(head_dim), s);
+  if (!ok) {
+    oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
+    return;
+  }
+  oxide::check_launch();
+}
+
+}  // namespace
+
+extern "C" void paged_prefill_attention(void* out, const void* q, const void* k_cache,
+                                        const void* v_cache, const uint32_t* cu_seqlens_q,
+                                        const uint32_t* cu_seqlens_k, const int32_t* block_table,
+                                        int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
+                                        int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                        int64_t page_block_size, int64_t max_seqlen_q,
+                                        int64_t max_seqlen_k, int32_t window_left,
+                                        float softmax_scale, int dtype, void* stream) {
+  if (block_table == nullptr && max_seqlen_k > 0) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  prefill_impl(out, q, k_cache, v_cache, cu_seqlens_q, cu_seqlens_k, block_table, max_blocks_per_seq,
+               num_blocks, 0, batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_q,
+               max_seqlen_k, window_left, softmax_scale, dtype, stream);
+}
+
+extern "C" void varlen_prefill_attention(void* out, const void* q, const void* k, const void* v,
+                                         const uint32_t* cu_seqlens_q, const uint32_t* cu_seqlens_k,
+                                         int64_t total_k, int64_t batch, int64_t num_heads,
+                                         int64_t num_kv_heads, int64_t head_dim, int64_t max_seqlen_q,
+                                         int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
+                                         int dtype, void* stream) {
+  prefill_impl(out, q, k, v, cu_seqlens_q, cu_seqlens_k, nullptr, 0, 0, total_k, batch, num_heads,
+               num_kv_heads, head_dim, 1, max_seqlen_q, max_seqlen_k, window_left, softmax_scale,
+               dtype, stream);
+}

@@ -5,6 +5,9 @@
 * decode_attn mirrors flash_attn_varlen_paged_windowed as called at
   crates/vllm-oxide/src/attention/flash_attn.rs:39-68 (the callee allocates the output).
 * gather_blocks is the prefix-hit gather (no reference counterpart).
+* prefill_attn mirrors prefill_attn (flash_attn.rs:15-37, flash_attn_varlen, causal) over
+  contiguous K/V, and, given a block table, the seqlen_q >= 1 call of
+  flash_attn_varlen_paged_windowed (flash_attn.rs:52-67) over the paged cache.
 
 Tensors must be contiguous CUDA (HIP) tensors; every call goes to the HIP library
 on torch's current stream and raises OxideError if the library reports an error.
@@ -138,6 +141,49 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
             raise _lib.OxideError("append needs key/value [B, Hkv, D] and int64 slot_mapping [B]")
         L.paged_decode_attention_append(_ptr(out), _ptr(q), _ptr(key), _ptr(value),
                                         _ptr(slot_mapping), *tail)
+    _lib.check()
+    return out
+
+
+def prefill_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                 cu_seqlens_k: torch.Tensor, max_seqlen_q: int, max_seqlen_k: int,
+                 softmax_scale: float, block_table: torch.Tensor | None = None,
+                 window_left: int | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Causal varlen prefill attention, masks aligned bottom-right (FlashAttention 2).
+
+    q [total_q, Hq, D].  With block_table (int32 [B, max_blocks], 0-padded), k/v are the
+    paged caches [NB, BS, Hkv, D]; without, contiguous [total_k, Hkv, D].  cu_seqlens_q /
+    cu_seqlens_k are 32-bit [B + 1] (uint32 bits).  window_left None = unbounded.
+    """
+    L = _lib.load()
+    Tq, Hq, D = q.shape
+    if cu_seqlens_q.dtype not in (torch.int32, torch.uint32) or \
+            cu_seqlens_k.dtype not in (torch.int32, torch.uint32):
+        raise _lib.OxideError("cu_seqlens_q / cu_seqlens_k must be 32-bit")
+    if k.dtype != q.dtype or v.dtype != q.dtype or v.shape != k.shape:
+        raise _lib.OxideError("q, k and v must share a dtype and k/v a shape")
+    B = cu_seqlens_q.shape[0] - 1
+    if cu_seqlens_k.shape[0] != B + 1:
+        raise _lib.OxideError("cu_seqlens_q and cu_seqlens_k disagree on the batch")
+    if out is None:
+        out = torch.empty_like(q)
+    w = -1 if window_left is None else int(window_left)
+    if block_table is not None:
+        NB, BS, Hkv, D2 = k.shape
+        if D2 != D or block_table.dtype != torch.int32:
+            raise _lib.OxideError("k_cache [NB, BS, Hkv, D] and int32 block_table expected")
+        max_blocks = block_table.shape[1] if block_table.dim() == 2 else 0
+        L.paged_prefill_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(cu_seqlens_q),
+                                  _ptr(cu_seqlens_k), _ptr(block_table), max_blocks, NB, B, Hq, Hkv,
+                                  D, BS, max_seqlen_q, max_seqlen_k, w, float(softmax_scale),
+                                  dtype_code(q.dtype), _stream(q))
+    else:
+        Tk, Hkv, D2 = k.shape
+        if D2 != D:
+            raise _lib.OxideError("k [total_k, Hkv, D] expected")
+        L.varlen_prefill_attention(_ptr(out), _ptr(q), _ptr(k), _ptr(v), _ptr(cu_seqlens_q),
+                                   _ptr(cu_seqlens_k), Tk, B, Hq, Hkv, D, max_seqlen_q, max_seqlen_k,
+                                   w, float(softmax_scale), dtype_code(q.dtype), _stream(q))
     _lib.check()
     return out
 
