@@ -52,9 +52,12 @@ __device__ __forceinline__ uint2 lds_read_tr16(const char* p) {
   return __builtin_bit_cast(uint2, r);
 }
 
-// Two fp32 probabilities -> packed 16-bit pair of the MFMA input type.
+// Two fp32 values -> packed 16-bit pair of the MFMA input type, round to
+// nearest even (bf16: one v_cvt_pk_bf16_f32).
+typedef float float2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack2(Bf16Tag, float lo, float hi) {
-  return static_cast<uint32_t>(pack1(Bf16Tag{}, lo)) | (static_cast<uint32_t>(pack1(Bf16Tag{}, hi)) << 16);
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((float2_t){lo, hi}, bf16x2_t));
 }
 __device__ __forceinline__ uint32_t pack2(F16Tag, float lo, float hi) {
   return static_cast<uint32_t>(pack1(F16Tag{}, lo)) | (static_cast<uint32_t>(pack1(F16Tag{}, hi)) << 16);

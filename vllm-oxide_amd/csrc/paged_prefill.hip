@@ -79,18 +79,49 @@ __device__ __forceinline__ int clamp_len(int64_t n, int cap) {
   return static_cast<int>(n < 0 ? 0 : (n > cap ? cap : n));
 }
 
-template <class Tag, int D>
-__global__ __launch_bounds__(kPfThreads) void paged_prefill_attn(PrefillParams p) {
+// LDS tile layouts (64 keys, row = one key's head slice of 2*D bytes):
+//   K: 16-byte chunk c of row r at chunk position c ^ (r % CH), so the 16 rows
+//      one MFMA operand read touches hit distinct banks;
+//   V: 32-byte granule g of row r at granule position g ^ vswz(r), so the
+//      16 rows x 32 bytes of one transposing read hit distinct banks.
+// Both are written by direct global -> LDS loads (global_load_lds_dwordx4):
+// lane i of a wave instruction fills bytes [16 i, 16 i + 16) of a 1 KiB run,
+// so each lane loads the source chunk that belongs at its LDS position.
+template <int D>
+__device__ __forceinline__ int vswz(int r) {
+  return D == 128 ? (r & 7) : ((r >> 1) & 3);
+}
+
+// One direct global -> LDS load of 16 bytes per lane: lane i writes LDS bytes
+// [lds + 16 i, lds + 16 i + 16).  Issued as inline assembly so the compiler
+// does not treat the in-flight loads as possibly aliasing the other buffer's
+// LDS reads (it otherwise waits for them before some transposing reads); the
+// kernel waits for them itself (vmcnt(0) before the barrier that publishes
+// the tile).  `lds` must be wave-uniform.
+__device__ __forceinline__ void load_lds16(const void* src, const char* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src)
+               : "memory", "m0");
+}
+
+template <class Tag, int D, bool PAGED>
+__global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParams p) {
   constexpr int CH = D / 8;                  // 16-byte chunks per head row
   constexpr int KK = D / 32;                 // MFMA k-steps of Q.K
-  constexpr int NDB = D / 16;                // 16-wide d blocks of the output
-  constexpr int VRS = 2 * D + 32;            // padded V row in LDS (bytes)
-  constexpr int KT_BYTES = kPfKeys * D * 2;
-  constexpr int BUF = KT_BYTES + kPfKeys * VRS;
-  constexpr int RPI = kPfThreads / CH;       // tile rows per load instruction
-  constexpr int NLD = kPfKeys / RPI;         // load instructions per tensor and tile
-  static_assert(kPfKeys % RPI == 0, "tile rows");
-  __shared__ __align__(16) char smem[2 * BUF];
+  constexpr int NDB = D / 16;                // 16-wide d blocks (= 32-byte V granules)
+  constexpr int ROWB = 2 * D;                // bytes per tile row
+  constexpr int TBYTES = kPfKeys * ROWB;     // one K or V tile
+  constexpr int BUF = 2 * TBYTES;            // K tile | V tile
+  constexpr int RPI = 1024 / ROWB;           // tile rows per wave load instruction
+  constexpr int WROWS = kPfKeys / kPfWaves;  // tile rows loaded by each wave
+  constexpr int NLD = WROWS / RPI;           // load instructions per wave and tensor
+  static_assert(WROWS % RPI == 0, "tile rows");
+  // Two LDS buffers as separate objects: the loop is unrolled by two so each
+  // access names its buffer statically, which lets the compiler see that the
+  // loads in flight into one buffer do not alias reads of the other.
+  __shared__ __align__(1024) char smem0[BUF];
+  __shared__ __align__(1024) char smem1[BUF];
 
   // XCD-aware work item: unit (sequence, kv head) u sits on XCD u % 8 and its
   // tiles are consecutive workgroups there, heaviest first.
@@ -145,43 +176,72 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_attn(PrefillParams p
   const int wave_hi = min(Lk - 1, wt_last + off);
   const int wave_lo = W >= 0 ? wt_first + off - W : 0;
 
+  // Queries (B operand of S^T).  A negative scale is applied as a sign flip of
+  // q (exact) and |scale|, so the running maxima can be taken on raw scores.
+  const uint32_t qflip = p.scale_log2 < 0.f ? 0x80008000u : 0u;
+  const float c_log2 = fabsf(p.scale_log2);
   uint4 qb[2][KK];
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qrow[c] * D;
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qb[c][kk] = valid[c] ? *reinterpret_cast<const uint4*>(qp + 8 * (grp + 4 * kk)) : make_uint4(0, 0, 0, 0);
+    for (int kk = 0; kk < KK; ++kk) {
+      uint4 v = valid[c] ? *reinterpret_cast<const uint4*>(qp + 8 * (grp + 4 * kk)) : make_uint4(0, 0, 0, 0);
+      v.x ^= qflip; v.y ^= qflip; v.z ^= qflip; v.w ^= qflip;
+      qb[c][kk] = v;
+    }
   }
 
-  // Tile loads: lane -> (row, chunk) of the 64-key tile; keys past Lk - 1 read
-  // row Lk - 1 (finite data, masked in the scores).
-  const int ldch = threadIdx.x % CH;
-  const int ldrow = threadIdx.x / CH;
+  // Direct tile loads: wave w fills tile rows [16 w, 16 w + 16); lane -> (row
+  // within the 1 KiB run, 16-byte position), source chunk chosen by the swizzle.
+  const int lrow = lane / CH;         // row within the run
+  const int lpos = lane % CH;         // 16-byte position within the row
   const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
-  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + kh * D + 8 * ldch;
-  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + kh * D + 8 * ldch;
+  const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + kh * D;
+  const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + kh * D;
   const int32_t* bt = p.block_table ? p.block_table + b * p.max_blocks : nullptr;
   const int64_t kstart = p.cu_seqlens_k[b];
-  const bool paged = bt != nullptr;
-  uint4 kr[NLD], vr[NLD];
-#define OXIDE_PF_LOAD_TILE(KB0)                                                              \
-  _Pragma("unroll") for (int x = 0; x < NLD; ++x) {                                          \
-    const int key = min((KB0) + ldrow + RPI * x, Lk - 1);                                    \
-    const int blk = paged ? min(max(bt[key / p.block_size], 0), p.num_blocks - 1) : 0;       \
-    const int64_t row = paged ? static_cast<int64_t>(blk) * p.block_size + key % p.block_size \
-                              : min(kstart + key, p.num_rows - 1);                           \
-    kr[x] = *reinterpret_cast<const uint4*>(kbase + row * row_stride);                       \
-    vr[x] = *reinterpret_cast<const uint4*>(vbase + row * row_stride);                       \
+  int kchunk[NLD], vchunk[NLD], blk_next[NLD];
+#pragma unroll
+  for (int x = 0; x < NLD; ++x) {
+    const int row = wave * WROWS + x * RPI + lrow;
+    kchunk[x] = 8 * (lpos ^ (row % CH));
+    vchunk[x] = 16 * ((lpos >> 1) ^ vswz<D>(row)) + 8 * (lpos & 1);
+    blk_next[x] = 0;
   }
-#define OXIDE_PF_STORE_TILE(BUFI)                                                            \
-  _Pragma("unroll") for (int x = 0; x < NLD; ++x) {                                          \
-    const int row = ldrow + RPI * x;                                                         \
-    reinterpret_cast<uint4*>(smem + (BUFI) * BUF)[row * CH + (ldch ^ (row % CH))] = kr[x];   \
-    *reinterpret_cast<uint4*>(smem + (BUFI) * BUF + KT_BYTES + row * VRS + 16 * ldch) = vr[x]; \
-  }
+  // Block-table entries of this lane's rows of the tile at kb0, read one tile
+  // ahead of its loads so their latency hides behind a whole tile of math.
+  auto fetch_blocks = [&](int kb0) {
+    if (!PAGED) return;
+#pragma unroll
+    for (int x = 0; x < NLD; ++x) {
+      const int key = min(kb0 + wave * WROWS + x * RPI + lrow, Lk - 1);
+      blk_next[x] = bt[key / p.block_size];
+    }
+  };
+  auto issue_tile = [&](int kb0, char* sbuf) {
+    // All source rows first, then the loads back to back.
+    int64_t rows[NLD];
+#pragma unroll
+    for (int x = 0; x < NLD; ++x) {
+      const int key = min(kb0 + wave * WROWS + x * RPI + lrow, Lk - 1);
+      if (PAGED) {
+        const int blk = min(max(blk_next[x], 0), p.num_blocks - 1);
+        rows[x] = static_cast<int64_t>(blk) * p.block_size + key % p.block_size;
+      } else {
+        rows[x] = min(kstart + key, p.num_rows - 1);
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < NLD; ++x) {
+      const int64_t row = rows[x];
+      char* dst = sbuf + (wave * WROWS + x * RPI) * ROWB;
+      load_lds16(kbase + row * row_stride + kchunk[x], dst);
+      load_lds16(vbase + row * row_stride + vchunk[x], dst + TBYTES);
+    }
+  };
 
-  float m_r[2] = {-INFINITY, -INFINITY};
+  float m_r[2] = {-INFINITY, -INFINITY};  // running max of raw scores (x |scale| log2 e)
   float l_r[2] = {0.f, 0.f};
   floatx4 acc[2][NDB];
 #pragma unroll
@@ -189,20 +249,16 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_attn(PrefillParams p
 #pragma unroll
     for (int db = 0; db < NDB; ++db) acc[c][db] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  if (ntiles > 0) {
-    OXIDE_PF_LOAD_TILE(kt0)
-    OXIDE_PF_STORE_TILE(0)
-  }
-  __syncthreads();
-  for (int it = 0; it < ntiles; ++it) {
+  auto step = [&](int it, char* cur, char* nxt) {
     const int kb0 = kt0 + it * kPfKeys;
-    const bool more = it + 1 < ntiles;
-    // The next tile, or (last iteration) this tile again from L2: an
-    // unconditional load keeps kr / vr in registers.
-    OXIDE_PF_LOAD_TILE(more ? kb0 + kPfKeys : kb0)
+    // Tile it has landed in LDS (own loads, then everyone's); then start the
+    // next tile into the other buffer, whose readers finished before this barrier.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (it + 1 < ntiles) issue_tile(kb0 + kPfKeys, nxt);
     if (wave_active && kb0 <= wave_hi && kb0 + kPfKeys - 1 >= wave_lo) {
-      const uint4* sk = reinterpret_cast<const uint4*>(smem + (it & 1) * BUF);
-      const char* sv = smem + (it & 1) * BUF + KT_BYTES;
+      const uint4* sk = reinterpret_cast<const uint4*>(cur);
+      const char* sv = cur + TBYTES;
 
       // Scores of 4 key blocks x 2 row blocks.
       floatx4 sc[2][4];
@@ -227,37 +283,48 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_attn(PrefillParams p
       uint4 pb[2][2];
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        float x[4][4];
+        if (need_mask) {
+          const int k0 = kb0 + 4 * grp;
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int key = k0 + kb * 16 + e;
+              sc[c][kb][e] = (key > hi_r[c] || key < lo_r[c]) ? -INFINITY : sc[c][kb][e];
+            }
+        }
         float mt = -INFINITY;
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            float s = sc[c][kb][e] * p.scale_log2;
-            if (need_mask) {
-              const int key = kb0 + kb * 16 + 4 * grp + e;
-              if (key > hi_r[c] || key < lo_r[c]) s = -INFINITY;
-            }
-            x[kb][e] = s;
-            mt = fmaxf(mt, s);
-          }
+          for (int e = 0; e < 4; ++e) mt = fmaxf(mt, sc[c][kb][e]);
         mt = fmaxf(mt, __shfl_xor(mt, 16));
         mt = fmaxf(mt, __shfl_xor(mt, 32));
-        const float mnew = fmaxf(m_r[c], mt);
-        const float msafe = mnew == -INFINITY ? 0.f : mnew;
-        const float alpha = __builtin_amdgcn_exp2f(m_r[c] - msafe);
+        // Lazy rescaling: keep the old maximum while the tile's stays within
+        // 2^8 of it (probabilities <= 256, exact in fp32 and bf16 range), so
+        // most tiles skip the 32 accumulator multiplies.
+        const float ms = mt * c_log2;
+        const bool grow = ms > m_r[c] + 8.f;
+        float alpha = 1.f;
+        if (grow) {
+          alpha = __builtin_amdgcn_exp2f(m_r[c] - ms);
+          m_r[c] = ms;
+        }
+        if (__ballot(grow) != 0) {
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) acc[c][db] *= alpha;
+        }
+        const float msafe = m_r[c] == -INFINITY ? 0.f : m_r[c];
         float psum = 0.f;
+        float x[4][4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            x[kb][e] = __builtin_amdgcn_exp2f(x[kb][e] - msafe);
+            x[kb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][kb][e], c_log2, -msafe));
             psum += x[kb][e];
           }
         l_r[c] = l_r[c] * alpha + psum;
-        m_r[c] = mnew;
-#pragma unroll
-        for (int db = 0; db < NDB; ++db) acc[c][db] *= alpha;
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           pb[c][s2].x = pack2(Tag{}, x[2 * s2][0], x[2 * s2][1]);
@@ -267,25 +334,37 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_attn(PrefillParams p
         }
       }
 
-      // O^T += V^T . P^T over two 32-key steps.
+      // O^T += V^T . P^T over two 32-key steps; lane i of group g reads row
+      // 4g + i/4 (+16), logical granule db, bytes 8 (i % 4).
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const char* vlo = sv + (32 * s2 + 4 * grp + r16 / 4) * VRS + 8 * (r16 % 4);
-        const char* vhi = vlo + 16 * VRS;
+        const int rlo = 32 * s2 + 4 * grp + r16 / 4;
+        const char* vlo = sv + rlo * ROWB + 8 * (r16 % 4);
+        const char* vhi = vlo + 16 * ROWB;
+        const int zlo = vswz<D>(rlo), zhi = vswz<D>(rlo + 16);
 #pragma unroll
         for (int db = 0; db < NDB; ++db) {
-          const uint2 a0 = lds_read_tr16(vlo + 32 * db);
-          const uint2 a1 = lds_read_tr16(vhi + 32 * db);
+          const uint2 a0 = lds_read_tr16(vlo + 32 * (db ^ zlo));
+          const uint2 a1 = lds_read_tr16(vhi + 32 * (db ^ zhi));
           const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
           acc[0][db] = mfma16x16x32(Tag{}, va, pb[0][s2], acc[0][db]);
           acc[1][db] = mfma16x16x32(Tag{}, va, pb[1][s2], acc[1][db]);
         }
       }
     }
-    if (more) {
-      OXIDE_PF_STORE_TILE((it + 1) & 1)
-    }
-    __syncthreads();
+    // Block-table entries for the tile after next, once this tile's LDS reads
+    // are issued (they complete under the next barrier's wait).
+    if (it + 2 < ntiles) fetch_blocks(kb0 + 2 * kPfKeys);
+  };
+  if (ntiles > 0) {
+    fetch_blocks(kt0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    issue_tile(kt0, smem0);
+    if (ntiles > 1) fetch_blocks(kt0 + kPfKeys);
+  }
+  for (int it = 0; it < ntiles; it += 2) {
+    step(it, smem0, smem1);
+    if (it + 1 < ntiles) step(it + 1, smem1, smem0);
   }
 
   // Row totals (the 4 lane groups of a column hold disjoint keys), then
@@ -306,8 +385,6 @@ __global__ __launch_bounds__(kPfThreads) void paged_prefill_attn(PrefillParams p
       *reinterpret_cast<uint2*>(op + 16 * db) = w;
     }
   }
-#undef OXIDE_PF_LOAD_TILE
-#undef OXIDE_PF_STORE_TILE
 }
 
 int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
@@ -316,12 +393,19 @@ template <class Tag>
 bool launch_prefill(const PrefillParams& p, int head_dim, hipStream_t s) {
   const int64_t units8 = ceil_div64(p.units, kPfXcds) * kPfXcds;
   const dim3 grid(static_cast<unsigned>(units8 * p.tiles_per_unit));
+  const bool paged = p.block_table != nullptr;
   if (head_dim == 128) {
-    hipLaunchKernelGGL((paged_prefill_attn<Tag, 128>), grid, dim3(kPfThreads), 0, s, p);
+    if (paged)
+      hipLaunchKernelGGL((paged_prefill_attn<Tag, 128, true>), grid, dim3(kPfThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((paged_prefill_attn<Tag, 128, false>), grid, dim3(kPfThreads), 0, s, p);
     return true;
   }
   if (head_dim == 64) {
-    hipLaunchKernelGGL((paged_prefill_attn<Tag, 64>), grid, dim3(kPfThreads), 0, s, p);
+    if (paged)
+      hipLaunchKernelGGL((paged_prefill_attn<Tag, 64, true>), grid, dim3(kPfThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((paged_prefill_attn<Tag, 64, false>), grid, dim3(kPfThreads), 0, s, p);
     return true;
   }
   return false;
