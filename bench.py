@@ -11,6 +11,10 @@ N(0,1) data resident in HBM, steps rotating over distinct layers of the
 [2, layers, NB, 256, 8, 128] buffer so that no step re-reads what the previous
 one left in the 256 MB MALL.
 
+With --prefill the step is instead one paged prefill attention call (causal,
+masks aligned bottom-right) over prompts whose K/V are already in the cache, at
+the Qwen3-8B head shape; its roofline is the matrix cores (bf16 dense peak).
+
 Prints ONE JSON line.  value = algorithmic bytes of (append + attention) per
 step / wall time per step.  The attention call (split-KV kernel + LSE merge
 kernel) is also timed with HIP events on the stream it runs on -> roofline.
@@ -93,6 +97,114 @@ def cpu_baseline(cfg, seed: int, threads: int, min_seconds: float = 10.0) -> dic
                       f"append + fp32-accumulated attention, {reps} reps in {dt:.1f} s"}
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
+
+
+def prefill_flops(lq: int, lk: int, heads: int, head_dim: int, window: int = -1) -> int:
+    """QK^T + PV flops of one sequence over the keys each query sees (masked keys excluded)."""
+    keys = 0
+    for i in range(lq):
+        hi = i + lk - lq
+        lo = 0 if window < 0 else max(0, hi - window)
+        keys += max(0, hi - lo + 1) if hi >= 0 else 0
+    return 4 * head_dim * heads * keys
+
+
+def prefill_cpu_baseline(seed: int, threads: int, min_seconds: float = 10.0) -> dict:
+    """Oracle prefill attention on one 512-token prompt of the same head shape."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(seed)
+    L, Hq, Hkv, D, BS = 512, 32, 8, 128, 256
+
+    def bits(shape):
+        return oracle.f32_to_bf16_bits(rng.standard_normal(size=shape, dtype=np.float32)).reshape(shape)
+
+    nb = L // BS
+    kc, vc, q = bits((nb, BS, Hkv, D)), bits((nb, BS, Hkv, D)), bits((L, Hq, D))
+    table = np.arange(nb, dtype=np.int32)[None]
+    cu = np.array([0, L], np.uint32)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.prefill_attention(q, kc, vc, cu, cu, 1 / math.sqrt(D), table, -1, "bf16", threads=threads)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            break
+    flops = prefill_flops(L, L, Hq, D)
+    return {"value": round(flops * reps / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"one {L}-token prompt, Qwen3-8B heads, fp32-accumulated, {reps} reps in {dt:.1f} s"}
+
+
+def prefill_main(args) -> int:
+    import torch
+
+    import oxide_paged_kv as ox
+
+    dev = torch.device("cuda:0")
+    B, Lq, P = args.prompts, args.prompt_len, args.prefix
+    Lk = Lq + P
+    Hq, Hkv, D, BS = 32, 8, 128, 256
+    nb = (Lk + BS - 1) // BS
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    layers = 2
+    kc = torch.randn((layers, B * nb, BS, Hkv, D), generator=g, device=dev).bfloat16()
+    vc = torch.randn((layers, B * nb, BS, Hkv, D), generator=g, device=dev).bfloat16()
+    q = torch.randn((layers, B * Lq, Hq, D), generator=g, device=dev).bfloat16()
+    perm = torch.randperm(B * nb, generator=torch.Generator().manual_seed(args.seed)).int()
+    table = perm.view(B, nb).to(dev)
+    cuq = (torch.arange(B + 1, dtype=torch.int32) * Lq).to(dev)
+    cuk = (torch.arange(B + 1, dtype=torch.int32) * Lk).to(dev)
+    out = torch.empty((B * Lq, Hq, D), dtype=torch.bfloat16, device=dev)
+    scale = 1 / math.sqrt(D)
+
+    def call(i):
+        ox.prefill_attn(q[i % layers], kc[i % layers], vc[i % layers], cuq, cuk, Lq, Lk, scale, table,
+                        None, out)
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(args.steps):
+        call(i)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us = e0.elapsed_time(e1) / args.steps * 1e3
+    flops = B * prefill_flops(Lq, Lk, Hq, D)
+    tflops = flops / (us * 1e-6) / 1e12
+    res = {
+        "metric": "paged prefill attention TFLOP/s (causal, Qwen3-8B heads)",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1) Q/K/V, seeded random block tables",
+        "config": {"workload": f"prefill-qwen3-8b-{B}x{Lq}" + (f"-prefix{P}" if P else ""),
+                   "prompts": B, "prompt_len": Lq, "prefix": P, "num_heads": Hq, "num_kv_heads": Hkv,
+                   "head_dim": D, "block_size": BS},
+        "call_us": round(us, 2),
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "kernel": "paged_prefill_attn", "algorithmic_flops": flops},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = prefill_cpu_baseline(args.seed, min(16, os.cpu_count() or 1))
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -104,11 +216,18 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate", action="store_true",
                     help="append and attention as two calls (default: one fused call)")
+    ap.add_argument("--prefill", action="store_true",
+                    help="time paged prefill attention instead of the decode step")
+    ap.add_argument("--prompts", type=int, default=4, help="--prefill: prompts per call")
+    ap.add_argument("--prompt-len", type=int, default=4096, help="--prefill: new tokens per prompt")
+    ap.add_argument("--prefix", type=int, default=0, help="--prefill: cached tokens before each prompt")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
         return 2
+    if args.prefill:
+        return prefill_main(args)
 
     import numpy as np
     import torch

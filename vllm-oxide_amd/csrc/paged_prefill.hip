@@ -39,6 +39,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "cdna4_tile.hpp"
 #include "oxide_common.hpp"
@@ -92,6 +93,10 @@ __device__ __forceinline__ int vswz(int r) {
   return D == 128 ? (r & 7) : ((r >> 1) & 3);
 }
 
+// 1.0 as a packed pair of the MFMA input type.
+template <class Tag>
+constexpr uint32_t kOnes16 = std::is_same<Tag, Bf16Tag>::value ? 0x3F803F80u : 0x3C003C00u;
+
 // One direct global -> LDS load of 16 bytes per lane: lane i writes LDS bytes
 // [lds + 16 i, lds + 16 i + 16).  Issued as inline assembly so the compiler
 // does not treat the in-flight loads as possibly aliasing the other buffer's
@@ -104,8 +109,22 @@ __device__ __forceinline__ void load_lds16(const void* src, const char* lds) {
   asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m0), "v"(src)
                : "memory", "m0");
 }
+// The same from a wave-uniform base address plus a 32-bit per-lane byte offset.
+__device__ __forceinline__ void load_lds16(const void* base, uint32_t voff, const char* lds) {
+  const uint32_t m0 = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds)));
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2" ::"s"(m0), "v"(voff), "s"(base)
+               : "memory", "m0");
+}
 
-template <class Tag, int D, bool PAGED>
+// K/V addressing of a kernel instance.
+enum PrefillAddressing {
+  kContiguous = 0,  // key j of sequence b at row cu_seqlens_k[b] + j
+  kPagedTiles = 1,  // paged, block_size a multiple of the 64-key tile: one block per tile
+  kPagedRows = 2,   // paged, any block_size: a block lookup per row
+};
+
+template <class Tag, int D, int MODE>
 __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParams p) {
   constexpr int CH = D / 8;                  // 16-byte chunks per head row
   constexpr int KK = D / 32;                 // MFMA k-steps of Q.K
@@ -180,17 +199,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   // q (exact) and |scale|, so the running maxima can be taken on raw scores.
   const uint32_t qflip = p.scale_log2 < 0.f ? 0x80008000u : 0u;
   const float c_log2 = fabsf(p.scale_log2);
-  uint4 qb[2][KK];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qrow[c] * D;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      uint4 v = valid[c] ? *reinterpret_cast<const uint4*>(qp + 8 * (grp + 4 * kk)) : make_uint4(0, 0, 0, 0);
-      v.x ^= qflip; v.y ^= qflip; v.z ^= qflip; v.w ^= qflip;
-      qb[c][kk] = v;
-    }
-  }
+  uint4 qb[2][KK];  // loaded after the first tile's loads are issued
 
   // Direct tile loads: wave w fills tile rows [16 w, 16 w + 16); lane -> (row
   // within the 1 KiB run, 16-byte position), source chunk chosen by the swizzle.
@@ -199,50 +208,79 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + kh * D;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + kh * D;
-  const int32_t* bt = p.block_table ? p.block_table + b * p.max_blocks : nullptr;
+  const int32_t* bt = p.block_table + (MODE == kContiguous ? 0 : b * p.max_blocks);
   const int64_t kstart = p.cu_seqlens_k[b];
-  int kchunk[NLD], vchunk[NLD], blk_next[NLD];
+  // Per-lane constants: tile row of each load, its byte offset in the tile's
+  // source rows, and the swizzled source chunks.
+  int trow[NLD];
+  uint32_t koff[NLD], voff[NLD], kchb[NLD], vchb[NLD];
+  int blk_next[NLD];
 #pragma unroll
   for (int x = 0; x < NLD; ++x) {
-    const int row = wave * WROWS + x * RPI + lrow;
-    kchunk[x] = 8 * (lpos ^ (row % CH));
-    vchunk[x] = 16 * ((lpos >> 1) ^ vswz<D>(row)) + 8 * (lpos & 1);
+    trow[x] = wave * WROWS + x * RPI + lrow;
+    kchb[x] = 16 * (lpos ^ (trow[x] % CH));
+    vchb[x] = 32 * ((lpos >> 1) ^ vswz<D>(trow[x])) + 16 * (lpos & 1);
+    koff[x] = static_cast<uint32_t>(trow[x] * row_stride * 2) + kchb[x];
+    voff[x] = static_cast<uint32_t>(trow[x] * row_stride * 2) + vchb[x];
     blk_next[x] = 0;
   }
-  // Block-table entries of this lane's rows of the tile at kb0, read one tile
-  // ahead of its loads so their latency hides behind a whole tile of math.
+  // Block-table entries of the tile at kb0 (one per tile, or one per row),
+  // read a tile ahead of its loads so their latency hides behind a tile of math.
   auto fetch_blocks = [&](int kb0) {
-    if (!PAGED) return;
+    if (MODE == kPagedTiles) {
+      blk_next[0] = bt[kb0 / p.block_size];
+    } else if (MODE == kPagedRows) {
 #pragma unroll
-    for (int x = 0; x < NLD; ++x) {
-      const int key = min(kb0 + wave * WROWS + x * RPI + lrow, Lk - 1);
-      blk_next[x] = bt[key / p.block_size];
+      for (int x = 0; x < NLD; ++x) blk_next[x] = bt[min(kb0 + trow[x], Lk - 1) / p.block_size];
     }
   };
   auto issue_tile = [&](int kb0, char* sbuf) {
-    // All source rows first, then the loads back to back.
-    int64_t rows[NLD];
+    if (MODE == kPagedRows) {
+      // General pages: a 64-bit source address per lane.
+      int64_t rows[NLD];
 #pragma unroll
-    for (int x = 0; x < NLD; ++x) {
-      const int key = min(kb0 + wave * WROWS + x * RPI + lrow, Lk - 1);
-      if (PAGED) {
+      for (int x = 0; x < NLD; ++x) {
+        const int key = min(kb0 + trow[x], Lk - 1);
         const int blk = min(max(blk_next[x], 0), p.num_blocks - 1);
         rows[x] = static_cast<int64_t>(blk) * p.block_size + key % p.block_size;
-      } else {
-        rows[x] = min(kstart + key, p.num_rows - 1);
       }
-    }
 #pragma unroll
-    for (int x = 0; x < NLD; ++x) {
-      const int64_t row = rows[x];
-      char* dst = sbuf + (wave * WROWS + x * RPI) * ROWB;
-      load_lds16(kbase + row * row_stride + kchunk[x], dst);
-      load_lds16(vbase + row * row_stride + vchunk[x], dst + TBYTES);
+      for (int x = 0; x < NLD; ++x) {
+        char* dst = sbuf + (wave * WROWS + x * RPI) * ROWB;
+        load_lds16(kbase + rows[x] * row_stride + kchb[x] / 2, dst);
+        load_lds16(vbase + rows[x] * row_stride + vchb[x] / 2, dst + TBYTES);
+      }
+    } else {
+      // The tile's rows are consecutive: a uniform base row plus per-lane
+      // offsets; rows past the last valid one repeat it.
+      int64_t row0;
+      int lim;  // last valid tile row
+      if (MODE == kPagedTiles) {
+        const int blk = min(max(__builtin_amdgcn_readfirstlane(blk_next[0]), 0), p.num_blocks - 1);
+        row0 = static_cast<int64_t>(blk) * p.block_size + kb0 % p.block_size;
+        lim = Lk - 1 - kb0;
+      } else {
+        row0 = min(kstart + kb0, p.num_rows - 1);
+        lim = static_cast<int>(min<int64_t>(Lk - 1 - kb0, p.num_rows - 1 - row0));
+      }
+      const uint32_t limb = static_cast<uint32_t>(lim * row_stride * 2);
+      const uint16_t* kt = kbase + row0 * row_stride;
+      const uint16_t* vt = vbase + row0 * row_stride;
+#pragma unroll
+      for (int x = 0; x < NLD; ++x) {
+        const bool in = trow[x] <= lim;
+        char* dst = sbuf + (wave * WROWS + x * RPI) * ROWB;
+        load_lds16(kt, in ? koff[x] : limb + kchb[x], dst);
+        load_lds16(vt, in ? voff[x] : limb + vchb[x], dst + TBYTES);
+      }
     }
   };
 
   float m_r[2] = {-INFINITY, -INFINITY};  // running max of raw scores (x |scale| log2 e)
-  float l_r[2] = {0.f, 0.f};
+  // Row sums of the probabilities on the matrix cores: a ones A operand times
+  // P^T puts the sum over the step's keys of row l%16 in every element.
+  const uint4 ones = make_uint4(kOnes16<Tag>, kOnes16<Tag>, kOnes16<Tag>, kOnes16<Tag>);
+  floatx4 lsum[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
   floatx4 acc[2][NDB];
 #pragma unroll
   for (int c = 0; c < 2; ++c)
@@ -313,18 +351,14 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
         if (__ballot(grow) != 0) {
 #pragma unroll
           for (int db = 0; db < NDB; ++db) acc[c][db] *= alpha;
+          lsum[c] *= alpha;
         }
         const float msafe = m_r[c] == -INFINITY ? 0.f : m_r[c];
-        float psum = 0.f;
         float x[4][4];
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            x[kb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][kb][e], c_log2, -msafe));
-            psum += x[kb][e];
-          }
-        l_r[c] = l_r[c] * alpha + psum;
+          for (int e = 0; e < 4; ++e) x[kb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][kb][e], c_log2, -msafe));
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
           pb[c][s2].x = pack2(Tag{}, x[2 * s2][0], x[2 * s2][1]);
@@ -350,6 +384,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
           acc[0][db] = mfma16x16x32(Tag{}, va, pb[0][s2], acc[0][db]);
           acc[1][db] = mfma16x16x32(Tag{}, va, pb[1][s2], acc[1][db]);
         }
+        lsum[0] = mfma16x16x32(Tag{}, ones, pb[0][s2], lsum[0]);
+        lsum[1] = mfma16x16x32(Tag{}, ones, pb[1][s2], lsum[1]);
       }
     }
     // Block-table entries for the tile after next, once this tile's LDS reads
@@ -358,22 +394,30 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   };
   if (ntiles > 0) {
     fetch_blocks(kt0);
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     issue_tile(kt0, smem0);
     if (ntiles > 1) fetch_blocks(kt0 + kPfKeys);
   }
+  // The queries load while the first tile is in flight.
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qrow[c] * D;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      uint4 v = valid[c] ? *reinterpret_cast<const uint4*>(qp + 8 * (grp + 4 * kk)) : make_uint4(0, 0, 0, 0);
+      v.x ^= qflip; v.y ^= qflip; v.z ^= qflip; v.w ^= qflip;
+      qb[c][kk] = v;
+    }
+  }
+
   for (int it = 0; it < ntiles; it += 2) {
     step(it, smem0, smem1);
     if (it + 1 < ntiles) step(it + 1, smem1, smem0);
   }
 
-  // Row totals (the 4 lane groups of a column hold disjoint keys), then
-  // out[row][d] for d = 16 db + 4 grp + e.
+  // out[row][d] for d = 16 db + 4 grp + e, normalised by the row total.
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    float l = l_r[c];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    const float l = lsum[c][0];
     if (!valid[c]) continue;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     uint16_t* op = static_cast<uint16_t*>(p.out) + qrow[c] * D + 4 * grp;
@@ -389,23 +433,26 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
 
 int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+template <class Tag, int D>
+void launch_mode(const PrefillParams& p, dim3 grid, hipStream_t s) {
+  if (p.block_table == nullptr)
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kContiguous>), grid, dim3(kPfThreads), 0, s, p);
+  else if (p.block_size % kPfKeys == 0)
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedTiles>), grid, dim3(kPfThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedRows>), grid, dim3(kPfThreads), 0, s, p);
+}
+
 template <class Tag>
 bool launch_prefill(const PrefillParams& p, int head_dim, hipStream_t s) {
   const int64_t units8 = ceil_div64(p.units, kPfXcds) * kPfXcds;
   const dim3 grid(static_cast<unsigned>(units8 * p.tiles_per_unit));
-  const bool paged = p.block_table != nullptr;
   if (head_dim == 128) {
-    if (paged)
-      hipLaunchKernelGGL((paged_prefill_attn<Tag, 128, true>), grid, dim3(kPfThreads), 0, s, p);
-    else
-      hipLaunchKernelGGL((paged_prefill_attn<Tag, 128, false>), grid, dim3(kPfThreads), 0, s, p);
+    launch_mode<Tag, 128>(p, grid, s);
     return true;
   }
   if (head_dim == 64) {
-    if (paged)
-      hipLaunchKernelGGL((paged_prefill_attn<Tag, 64, true>), grid, dim3(kPfThreads), 0, s, p);
-    else
-      hipLaunchKernelGGL((paged_prefill_attn<Tag, 64, false>), grid, dim3(kPfThreads), 0, s, p);
+    launch_mode<Tag, 64>(p, grid, s);
     return true;
   }
   return false;
