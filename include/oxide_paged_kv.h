@@ -217,6 +217,45 @@ void varlen_prefill_attention(void* out, const void* q, const void* k, const voi
                               int dtype, void* stream);
 
 /*
+ * The attention prologue fused with the KV append.  Replaces, per token t, the
+ * chain of Qwen3Attention::forward (crates/vllm-oxide/src/models/qwen3.rs:161-199):
+ * split of the merged qkv row, q_norm / k_norm (layers/rmsnorm.rs:52-87),
+ * rotary_emb.forward (layers/rope.rs:133-163) and
+ * PagedKVCache::reshape_and_cache(k, v, slot_mapping) (qwen3.rs:199).
+ *
+ *   q_out          [T, num_heads, head_dim]      written: normed + rotated q
+ *   k_out          [T, num_kv_heads, head_dim]   optional (NULL = not written)
+ *   qkv            [T, qkv_row_stride], row = q (Hq*D) | k (Hkv*D) | v (Hkv*D)
+ *   q_norm_weight, k_norm_weight   [head_dim] in the dtype, or NULL: no norm
+ *                  (Qwen3 with attention bias has none, qwen3.rs:118-136)
+ *   eps            rms_norm_eps
+ *   cos_sin_cache  fp32 [max_position, head_dim] (oxide_rope_cos_sin_cache);
+ *                  positions outside [0, max_position) are clamped into it
+ *   positions      int32 [T]
+ *   key_cache, value_cache, slot_mapping   as for reshape_and_cache; with
+ *                  slot_mapping == NULL nothing is appended
+ *
+ * Per head: x -> round(round(x / sqrt(mean(x^2) + eps)) * w), then
+ * y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin (halves x1 = x[:D/2],
+ * x2 = x[D/2:]), each product and sum rounded to fp32, y rounded to the dtype.
+ * v is copied bitwise.  Supported: f16/bf16, head_dim 64 or 128.
+ */
+void qk_norm_rope_and_cache(void* q_out, void* k_out, const void* qkv, int64_t qkv_row_stride,
+                            const void* q_norm_weight, const void* k_norm_weight, double eps,
+                            const float* cos_sin_cache, int64_t max_position,
+                            const int32_t* positions, void* key_cache, void* value_cache,
+                            const int64_t* slot_mapping, int64_t num_tokens, int64_t num_heads,
+                            int64_t num_kv_heads, int64_t head_dim, int dtype, void* stream);
+
+/*
+ * Host helper: fills `cache` (host memory, max_position * rotary_dim floats)
+ * with RotaryEmbedding's cos_sin_cache (crates/vllm-oxide/src/layers/rope.rs:50-83):
+ * row t = [cos(t f_i) | sin(t f_i)], f_i = 1 / base^(2i / rotary_dim), fp32.
+ * Returns OXIDE_OK or OXIDE_ERR_INVALID_ARGUMENT.
+ */
+int oxide_rope_cos_sin_cache(float* cache, int64_t max_position, int64_t rotary_dim, float base);
+
+/*
  * Decode metadata on the device (the reference builds it on the host in every
  * layer: crates/vllm-oxide/src/engine/mod.rs:247-267, metadata.rs:20-47,
  * kv_cache_manager.rs:115-135).  From context_lens (uint32 [batch], the new

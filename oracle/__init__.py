@@ -53,6 +53,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_prefill_attention.argtypes = [
             _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, ctypes.c_float,
             ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.oracle_rope_cos_sin_cache.argtypes = [_p, _i64, _i64, ctypes.c_float]
+        L.oracle_qk_norm_rope_and_cache.argtypes = [
+            _p, _p, _p, _i64, _p, _p, ctypes.c_double, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64,
+            _i64, ctypes.c_int]
         L.oracle_xxh64.restype = ctypes.c_uint64
         L.oracle_xxh64.argtypes = [_p, ctypes.c_size_t, ctypes.c_uint64]
         _lib = L
@@ -204,6 +208,32 @@ def prefill_attention(q, k, v, cu_seqlens_q, cu_seqlens_k, softmax_scale: float,
                                    maxb, B, Hq, Hkv, D, BS, window_left, softmax_scale,
                                    DTYPE_CODE[dtype], int(use_f64), threads)
     return out
+
+
+def rope_cos_sin_cache(max_position: int, rotary_dim: int, base: float) -> np.ndarray:
+    """RotaryEmbedding::new's cos_sin_cache (layers/rope.rs:50-83), fp32 [max_position, rotary_dim]."""
+    out = np.empty((max_position, rotary_dim), np.float32)
+    lib().oracle_rope_cos_sin_cache(_ptr(out), max_position, rotary_dim, base)
+    return out
+
+
+def qk_norm_rope_and_cache(qkv, num_heads: int, num_kv_heads: int, head_dim: int, q_norm_weight,
+                           k_norm_weight, eps: float, cos_sin_cache, positions, key_cache=None,
+                           value_cache=None, slot_mapping=None, dtype: str = "bf16"):
+    """Qwen3Attention::forward's prologue (models/qwen3.rs:161-199) on uint16 bit patterns:
+    returns (q_out [T, Hq, D], k_out [T, Hkv, D]) and appends k/v into the caches in place."""
+    T = qkv.shape[0]
+    qkv = np.ascontiguousarray(qkv)
+    q_out = np.empty((T, num_heads, head_dim), np.uint16)
+    k_out = np.empty((T, num_kv_heads, head_dim), np.uint16)
+    cs = np.ascontiguousarray(cos_sin_cache, np.float32)
+    pos = np.ascontiguousarray(positions, np.int32)
+    sm = None if slot_mapping is None else np.ascontiguousarray(slot_mapping, np.int64)
+    lib().oracle_qk_norm_rope_and_cache(_ptr(q_out), _ptr(k_out), _ptr(qkv), qkv.shape[1],
+                                        _ptr(q_norm_weight), _ptr(k_norm_weight), eps, _ptr(cs),
+                                        cs.shape[0], _ptr(pos), _ptr(key_cache), _ptr(value_cache),
+                                        _ptr(sm), T, num_heads, num_kv_heads, head_dim, DTYPE_CODE[dtype])
+    return q_out, k_out
 
 
 def xxh64(data: bytes, seed: int = 0) -> int:

@@ -22,6 +22,14 @@
  *                            decode oracle; the FlashAttention 2 bottom-right
  *                            mask on a hand-worked Lq = 2, Lk = 5 case; paged
  *                            equals contiguous; rows with no keys give zeros
+ *   rope_cos_sin_cache       numpy float32 restatement of the formula; the
+ *                            reference's own tests (position 0 row = [1.., 0..],
+ *                            shape, base changes the cache)
+ *   qk_norm_rope_and_cache   numpy fp64 RMSNorm + complex-multiplication RoPE
+ *                            with the same rounding points; position 0 is the
+ *                            identity after the norm (the reference's test);
+ *                            constant rows normalise to +-1; the rotation keeps
+ *                            each (x1_i, x2_i) pair's length; v copied bitwise
  *   xxh64                    python-xxhash digests and the spec's empty-input
  *                            vector
  */
@@ -359,6 +367,86 @@ void oracle_prefill_attention(float* out, const uint16_t* q, const uint16_t* k, 
     free(acc);
     free(accf);
   }
+}
+
+/* ------------------------------------------------------ norm + rope prologue */
+
+void oracle_rope_cos_sin_cache(float* cache, int64_t max_position, int64_t rotary_dim, float base) {
+  const int64_t half = rotary_dim / 2;
+  for (int64_t t = 0; t < max_position; ++t) {
+    for (int64_t i = 0; i < half; ++i) {
+      const float inv_freq = 1.0f / powf(base, (float)(2 * i) / (float)rotary_dim);
+      const float f = (float)t * inv_freq;
+      cache[t * rotary_dim + i] = cosf(f);
+      cache[t * rotary_dim + half + i] = sinf(f);
+    }
+  }
+}
+
+static float round_to(float x, int dtype) { return oracle_half_to_float(oracle_float_to_half(x, dtype), dtype); }
+
+/* layers/rmsnorm.rs:52-87 (residual None) on one head of D values. */
+static void rms_norm_head(float* x, const uint16_t* w, int64_t d, double eps, int dtype) {
+  double ss = 0.0;
+  for (int64_t i = 0; i < d; ++i) ss += (double)x[i] * (double)x[i];
+  const float var = (float)ss / (float)d;
+  const float s = sqrtf(var + (float)eps);
+  for (int64_t i = 0; i < d; ++i) {
+    const float n = round_to(x[i] / s, dtype);
+    x[i] = round_to(n * oracle_half_to_float(w[i], dtype), dtype);
+  }
+}
+
+/* layers/rope.rs:150-163 on one head (x holds dtype-rounded values). */
+static void rope_head(float* x, const float* cs, int64_t d, int dtype) {
+  const int64_t h = d / 2;
+  for (int64_t i = 0; i < h; ++i) {
+    const float x1 = x[i], x2 = x[h + i], c = cs[i], s = cs[h + i];
+    /* each product and sum rounded to fp32 (built with -ffp-contract=off) */
+    x[i] = round_to(x1 * c - x2 * s, dtype);
+    x[h + i] = round_to(x2 * c + x1 * s, dtype);
+  }
+}
+
+void oracle_qk_norm_rope_and_cache(uint16_t* q_out, uint16_t* k_out, const uint16_t* qkv,
+                                   int64_t qkv_stride, const uint16_t* q_norm_weight,
+                                   const uint16_t* k_norm_weight, double eps,
+                                   const float* cos_sin_cache, int64_t max_position,
+                                   const int32_t* positions, uint16_t* key_cache,
+                                   uint16_t* value_cache, const int64_t* slot_mapping,
+                                   int64_t num_tokens, int64_t num_heads, int64_t num_kv_heads,
+                                   int64_t head_dim, int dtype) {
+  const int64_t D = head_dim;
+  float* x = (float*)malloc(sizeof(float) * (size_t)D);
+  for (int64_t t = 0; t < num_tokens; ++t) {
+    int64_t pos = positions[t];
+    if (pos < 0) pos = 0;
+    if (pos >= max_position) pos = max_position - 1;
+    const float* cs = cos_sin_cache + pos * D;
+    const uint16_t* row = qkv + t * qkv_stride;
+    const int64_t slot = slot_mapping ? slot_mapping[t] : -1;
+    for (int64_t h = 0; h < num_heads + num_kv_heads; ++h) {
+      const int is_q = h < num_heads;
+      for (int64_t i = 0; i < D; ++i) x[i] = oracle_half_to_float(row[h * D + i], dtype);
+      const uint16_t* w = is_q ? q_norm_weight : k_norm_weight;
+      if (w) rms_norm_head(x, w, D, eps, dtype);
+      rope_head(x, cs, D, dtype);
+      if (is_q) {
+        for (int64_t i = 0; i < D; ++i) q_out[(t * num_heads + h) * D + i] = oracle_float_to_half(x[i], dtype);
+      } else {
+        const int64_t kh = h - num_heads;
+        for (int64_t i = 0; i < D; ++i) {
+          const uint16_t bits = oracle_float_to_half(x[i], dtype);
+          if (k_out) k_out[(t * num_kv_heads + kh) * D + i] = bits;
+          if (slot >= 0) key_cache[(slot * num_kv_heads + kh) * D + i] = bits;
+        }
+      }
+    }
+    if (slot >= 0)
+      memcpy(value_cache + slot * num_kv_heads * D, row + (num_heads + num_kv_heads) * D,
+             sizeof(uint16_t) * (size_t)(num_kv_heads * D));
+  }
+  free(x);
 }
 
 /* ------------------------------------------------------------------ XXH64 */

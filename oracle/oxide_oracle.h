@@ -92,6 +92,30 @@ void oracle_prefill_attention(float* out, const uint16_t* q, const uint16_t* k, 
                               int64_t block_size, int32_t window_left, float softmax_scale,
                               int dtype, int use_f64, int threads);
 
+/* RoPE cos/sin cache, layers/rope.rs:50-83: row t = [cos(t f_0..f_{R/2-1}),
+ * sin(...)], f_i = 1 / base^(2i / R) in fp32, t f_i rounded to fp32. */
+void oracle_rope_cos_sin_cache(float* cache, int64_t max_position, int64_t rotary_dim, float base);
+
+/* The attention prologue of Qwen3Attention::forward (models/qwen3.rs:161-199):
+ * split the merged qkv row [Hq*D | Hkv*D | Hkv*D] (row stride qkv_stride
+ * elements), RMSNorm q and k per head (layers/rmsnorm.rs:52-87: fp32 upcast,
+ * x / sqrt(mean(x^2) + eps), rounded to the dtype, times the weight, rounded;
+ * skipped when the weight pointer is NULL), RoPE by positions[t]
+ * (layers/rope.rs:133-163: y1 = x1 cos - x2 sin, y2 = x2 cos + x1 sin, each
+ * product and sum rounded to fp32, result rounded to the dtype), then
+ * reshape_and_cache of k and v at slot_mapping[t] (-1 skipped).  q_out
+ * [T, Hq, D]; k_out [T, Hkv, D] optional.  The mean of squares is summed in
+ * fp64 and rounded once to fp32 (the reference's reduction order is that of
+ * its backend). */
+void oracle_qk_norm_rope_and_cache(uint16_t* q_out, uint16_t* k_out, const uint16_t* qkv,
+                                   int64_t qkv_stride, const uint16_t* q_norm_weight,
+                                   const uint16_t* k_norm_weight, double eps,
+                                   const float* cos_sin_cache, int64_t max_position,
+                                   const int32_t* positions, uint16_t* key_cache,
+                                   uint16_t* value_cache, const int64_t* slot_mapping,
+                                   int64_t num_tokens, int64_t num_heads, int64_t num_kv_heads,
+                                   int64_t head_dim, int dtype);
+
 /* XXH64 (public xxHash spec, 64-bit variant) of `len` bytes with `seed`. */
 uint64_t oracle_xxh64(const void* data, size_t len, uint64_t seed);
 

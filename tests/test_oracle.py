@@ -323,3 +323,103 @@ def test_xxh64_matches_python_xxhash():
         data = rng.integers(0, 256, n).astype(np.uint8).tobytes()
         for seed in (0, 1, 2**63 + 5):
             assert oracle.xxh64(data, seed) == xxhash.xxh64_intdigest(data, seed=seed)
+
+
+# ------------------------------------------------------ norm + rope prologue
+def test_rope_cos_sin_cache_formula_and_reference_tests():
+    """layers/rope.rs:50-83: f_i = 1 / base^(2i/R) (fp32), row t = [cos(t f), sin(t f)].
+    The argument t*f_i is rounded to fp32 before cos/sin, so compare against float64
+    cos/sin of that same fp32 argument.  Plus the reference's own tests: shape, row 0 =
+    [1.., 0..], and the base changes the cache (rope.rs:176-258)."""
+    R, P = 128, 4096
+    cs = oracle.rope_cos_sin_cache(P, R, 1_000_000.0)
+    assert cs.shape == (P, R)
+    assert np.all(cs[0, :R // 2] == 1.0) and np.all(cs[0, R // 2:] == 0.0)
+    i = np.arange(R // 2, dtype=np.float32)
+    p32 = np.power(np.float64(1_000_000.0), ((2 * i) / np.float32(R)).astype(np.float64)).astype(np.float32)
+    inv = np.float32(1.0) / p32  # powf rounded to fp32, then an fp32 reciprocal
+    t = np.arange(P, dtype=np.float32)[:, None]
+    arg = (t * inv[None]).astype(np.float32).astype(np.float64)
+    np.testing.assert_allclose(cs[:, :R // 2], np.cos(arg), atol=2e-6)
+    np.testing.assert_allclose(cs[:, R // 2:], np.sin(arg), atol=2e-6)
+    assert not np.allclose(cs, oracle.rope_cos_sin_cache(P, R, 10_000.0))
+
+
+def _prologue_case(seed, T, Hq, Hkv, D, dtype="bf16", weights=True):
+    rng = np.random.default_rng(seed)
+    qkv = normal_bits(rng, (T, (Hq + 2 * Hkv) * D), dtype)
+    wq = normal_bits(rng, (D,), dtype, 0.1) if weights else None
+    wk = normal_bits(rng, (D,), dtype, 0.1) if weights else None
+    if weights:  # weights around 1 (trained norms)
+        wq = oracle.float_to_half(1.0 + oracle.half_to_float(wq, dtype), dtype)
+        wk = oracle.float_to_half(1.0 + oracle.half_to_float(wk, dtype), dtype)
+    pos = rng.integers(0, 4096, T).astype(np.int32)
+    return qkv, wq, wk, pos
+
+
+def _numpy_prologue(qkv, Hq, Hkv, D, wq, wk, eps, cs, pos, dtype):
+    """Independent vectorised restatement: fp64 mean of squares, float32 division by the
+    sqrt, dtype rounding, weight product, then RoPE as (x1 + i x2)(cos + i sin) with every
+    product and sum in float32."""
+    T = qkv.shape[0]
+    x = oracle.half_to_float(qkv[:, :(Hq + Hkv) * D], dtype).reshape(T, Hq + Hkv, D)
+    rnd = lambda a: oracle.half_to_float(oracle.float_to_half(a.astype(np.float32), dtype), dtype)  # noqa: E731
+    if wq is not None:
+        w = np.concatenate([np.repeat(oracle.half_to_float(wq, dtype)[None], Hq, 0),
+                            np.repeat(oracle.half_to_float(wk, dtype)[None], Hkv, 0)])[None]
+        var = ((x.astype(np.float64) ** 2).sum(-1, keepdims=True)).astype(np.float32) / np.float32(D)
+        s = np.sqrt(var + np.float32(eps), dtype=np.float32)
+        x = rnd(rnd(x / s) * w)
+    c = cs[pos][:, None, :D // 2]
+    sn = cs[pos][:, None, D // 2:]
+    x1, x2 = x[..., :D // 2], x[..., D // 2:]
+    y = np.concatenate([rnd(x1 * c - x2 * sn), rnd(x2 * c + x1 * sn)], -1)
+    bits = oracle.float_to_half(y, dtype)
+    return bits[:, :Hq], bits[:, Hq:]
+
+
+@pytest.mark.parametrize("D,dtype,weights", [(128, "bf16", True), (64, "f16", True), (128, "bf16", False)])
+def test_prologue_matches_numpy_and_appends(D, dtype, weights):
+    T, Hq, Hkv = 9, 4, 2
+    qkv, wq, wk, pos = _prologue_case(3, T, Hq, Hkv, D, dtype, weights)
+    cs = oracle.rope_cos_sin_cache(4096, D, 1_000_000.0)
+    NB, BS = 4, 16
+    kc = np.zeros((NB, BS, Hkv, D), np.uint16)
+    vc = np.zeros_like(kc)
+    slots = np.array([3, 17, -1, 40, 0, 63, 5, 6, 7], np.int64)
+    q, k = oracle.qk_norm_rope_and_cache(qkv, Hq, Hkv, D, wq, wk, 1e-6, cs, pos, kc, vc, slots, dtype)
+    wq_, wk_ = _numpy_prologue(qkv, Hq, Hkv, D, wq, wk, 1e-6, cs, pos, dtype)
+    assert np.array_equal(q, wq_) and np.array_equal(k, wk_)
+    kcf, vcf = kc.reshape(-1, Hkv, D), vc.reshape(-1, Hkv, D)
+    for t, s in enumerate(slots):
+        if s >= 0:
+            assert np.array_equal(kcf[s], k[t])
+            assert np.array_equal(vcf[s], qkv[t, (Hq + Hkv) * D:].reshape(Hkv, D))
+    written = set(int(s) for s in slots if s >= 0)
+    assert not kcf[[i for i in range(NB * BS) if i not in written]].any()
+
+
+def test_prologue_closed_forms():
+    """Position 0 is the identity after the norm (the reference's rope test,
+    rope.rs:205-223); a constant row with unit weights normalises to 1, and at
+    position p the pair (1, 1) turns into (cos - sin, cos + sin); the rotation keeps
+    each pair's length."""
+    T, Hq, Hkv, D = 4, 2, 1, 128
+    cs = oracle.rope_cos_sin_cache(4096, D, 1_000_000.0)
+    ones = oracle.float_to_half(np.ones(D, np.float32), "bf16")
+    qkv = oracle.float_to_half(np.full((T, (Hq + 2 * Hkv) * D), 3.0, np.float32), "bf16")
+    pos = np.array([0, 1, 100, 4095], np.int32)
+    q, k = oracle.qk_norm_rope_and_cache(qkv, Hq, Hkv, D, ones, ones, 1e-6, cs, pos)
+    qf = oracle.half_to_float(q, "bf16")
+    assert np.all(qf[0] == 1.0)
+    c, s = cs[pos, :D // 2], cs[pos, D // 2:]
+    np.testing.assert_allclose(qf[:, 0, :D // 2], c - s, atol=8e-3)
+    np.testing.assert_allclose(qf[:, 0, D // 2:], c + s, atol=8e-3)
+    # Random rows: the norm output at position 0 equals the rotated output's pair lengths.
+    qkv, wq, wk, _ = _prologue_case(4, 3, Hq, Hkv, D)
+    q0, _ = oracle.qk_norm_rope_and_cache(qkv, Hq, Hkv, D, wq, wk, 1e-6, cs, np.zeros(3, np.int32))
+    q1, _ = oracle.qk_norm_rope_and_cache(qkv, Hq, Hkv, D, wq, wk, 1e-6, cs, np.array([7, 300, 4000], np.int32))
+    a, b = oracle.half_to_float(q0, "bf16"), oracle.half_to_float(q1, "bf16")
+    la = np.hypot(a[..., :D // 2], a[..., D // 2:])
+    lb = np.hypot(b[..., :D // 2], b[..., D // 2:])
+    np.testing.assert_allclose(lb, la, rtol=2e-2, atol=1e-2)

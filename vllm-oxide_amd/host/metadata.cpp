@@ -1,9 +1,12 @@
 // Attention metadata, block-table padding, layout helpers and XXH64 (host).
 // Semantics follow crates/vllm-oxide/src/attention/metadata.rs:20-81,
 // attention/flash_attn.rs:74-86 and utils.rs:27-61.
+#include <algorithm>
+#include <cmath>
 #include <cstring>
 
 #include "oxide_host.hpp"
+#include "oxide_paged_kv.h"
 
 namespace oxide::host {
 
@@ -112,4 +115,26 @@ uint64_t xxh64(const void* data, std::size_t len, uint64_t seed) {
   return h;
 }
 
+std::vector<float> rope_cos_sin_cache(std::size_t max_position, std::size_t rotary_dim, float base) {
+  const std::size_t half = rotary_dim / 2;
+  std::vector<float> cache(max_position * rotary_dim);
+  for (std::size_t i = 0; i < half; ++i) {
+    const float inv_freq = 1.0f / std::pow(base, static_cast<float>(2 * i) / static_cast<float>(rotary_dim));
+    for (std::size_t t = 0; t < max_position; ++t) {
+      const float f = static_cast<float>(t) * inv_freq;
+      cache[t * rotary_dim + i] = std::cos(f);
+      cache[t * rotary_dim + half + i] = std::sin(f);
+    }
+  }
+  return cache;
+}
+
 }  // namespace oxide::host
+
+extern "C" int oxide_rope_cos_sin_cache(float* cache, int64_t max_position, int64_t rotary_dim, float base) {
+  if (!cache || max_position <= 0 || rotary_dim <= 0 || rotary_dim % 2 != 0) return OXIDE_ERR_INVALID_ARGUMENT;
+  const std::vector<float> c = oxide::host::rope_cos_sin_cache(static_cast<std::size_t>(max_position),
+                                                               static_cast<std::size_t>(rotary_dim), base);
+  std::copy(c.begin(), c.end(), cache);
+  return OXIDE_OK;
+}

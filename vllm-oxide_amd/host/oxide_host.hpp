@@ -11,6 +11,7 @@
 //   block_table_tensor padding crates/vllm-oxide/src/attention/flash_attn.rs:74-86
 //   kv_cache_layout_shape      crates/vllm-oxide/src/utils.rs:46-61
 //   PagedKVCache               crates/vllm-oxide/src/attention/mod.rs:48-112
+//   RotaryEmbedding cache      crates/vllm-oxide/src/layers/rope.rs:50-83
 // Fallible pool operations throw BlockPoolError where the reference returns
 // Err(BlockPoolError); the messages name the same conditions.
 #pragma once
@@ -39,6 +40,11 @@ std::size_t round_up(std::size_t x, std::size_t m);
 
 // XXH64 of `len` bytes (the 64-bit xxHash of the public specification).
 uint64_t xxh64(const void* data, std::size_t len, uint64_t seed);
+
+// RotaryEmbedding's cos_sin_cache (crates/vllm-oxide/src/layers/rope.rs:50-83):
+// [max_position, rotary_dim] fp32, row t = [cos(t f_i) | sin(t f_i)] with
+// f_i = 1 / base^(2i / rotary_dim), all in fp32.
+std::vector<float> rope_cos_sin_cache(std::size_t max_position, std::size_t rotary_dim, float base);
 
 // ------------------------------------------------------------------ metadata
 struct AttnMetadata {

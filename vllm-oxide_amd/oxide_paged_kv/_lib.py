@@ -36,6 +36,10 @@ SIGNATURES = {
     "varlen_prefill_attention": (None, [
         _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int32,
         ctypes.c_float, ctypes.c_int, _p]),
+    "qk_norm_rope_and_cache": (None, [
+        _p, _p, _p, _i64, _p, _p, ctypes.c_double, _p, _i64, _p, _p, _p, _p, _i64, _i64, _i64, _i64,
+        ctypes.c_int, _p]),
+    "oxide_rope_cos_sin_cache": (ctypes.c_int, [_p, _i64, _i64, ctypes.c_float]),
     "build_decode_metadata_device": (None, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
     "oxide_last_error": (ctypes.c_int, []),
     "oxide_clear_error": (None, []),

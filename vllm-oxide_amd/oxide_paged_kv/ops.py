@@ -188,6 +188,48 @@ def prefill_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens_q
     return out
 
 
+def rope_cos_sin_cache(max_position: int, rotary_dim: int, base: float = 1_000_000.0,
+                       device=None) -> torch.Tensor:
+    """RotaryEmbedding's fp32 cos_sin_cache [max_position, rotary_dim] (layers/rope.rs:50-83),
+    built on the host by the library and moved to `device`."""
+    L = _lib.load()
+    cache = torch.empty((max_position, rotary_dim), dtype=torch.float32)
+    rc = L.oxide_rope_cos_sin_cache(cache.data_ptr(), max_position, rotary_dim, float(base))
+    if rc != _lib.OXIDE_OK:
+        raise _lib.OxideError(f"oxide_rope_cos_sin_cache: error {rc}")
+    return cache.to(device) if device is not None else cache
+
+
+def qk_norm_rope_and_cache(qkv: torch.Tensor, num_heads: int, num_kv_heads: int,
+                           q_norm_weight: torch.Tensor | None, k_norm_weight: torch.Tensor | None,
+                           eps: float, cos_sin_cache: torch.Tensor, positions: torch.Tensor,
+                           key_cache: torch.Tensor | None = None, value_cache: torch.Tensor | None = None,
+                           slot_mapping: torch.Tensor | None = None, return_k: bool = False):
+    """Qwen3 attention prologue + KV append in one launch (models/qwen3.rs:161-199).
+
+    qkv [T, (Hq + 2 Hkv) D] (row = q | k | v); returns q [T, Hq, D] (and k [T, Hkv, D]
+    with return_k).  positions int32 [T]; cos_sin_cache fp32 [max_position, D];
+    key/value caches [NB, BS, Hkv, D] with int64 slot_mapping [T] (-1 = skip).
+    """
+    L = _lib.load()
+    T = qkv.shape[0]
+    D = cos_sin_cache.shape[1]
+    if positions.dtype != torch.int32 or cos_sin_cache.dtype != torch.float32:
+        raise _lib.OxideError("positions must be int32 and cos_sin_cache float32")
+    if slot_mapping is not None and slot_mapping.dtype != torch.int64:
+        raise _lib.OxideError("slot_mapping must be int64")
+    if qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise _lib.OxideError("qkv must be [T, row] with unit element stride")
+    q = torch.empty((T, num_heads, D), dtype=qkv.dtype, device=qkv.device)
+    k = torch.empty((T, num_kv_heads, D), dtype=qkv.dtype, device=qkv.device) if return_k else None
+    L.qk_norm_rope_and_cache(_ptr(q), _ptr(k), qkv.data_ptr(), qkv.stride(0), _ptr(q_norm_weight),
+                             _ptr(k_norm_weight), float(eps), _ptr(cos_sin_cache), cos_sin_cache.shape[0],
+                             _ptr(positions), _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping), T,
+                             num_heads, num_kv_heads, D, dtype_code(qkv.dtype), _stream(qkv))
+    _lib.check()
+    return (q, k) if return_k else q
+
+
 def build_decode_metadata(context_lens: torch.Tensor, block_table: torch.Tensor, block_size: int = 256):
     """Device-side decode metadata: (cu_seqlens_k [B+1] as int32 bits of uint32,
     slot_mapping int64 [B]) from context_lens (int32 bits of uint32, [B]) and the
