@@ -223,6 +223,53 @@ static void test_block_pool() {
 }
 
 // ------------------------------------------------------------------- GPU
+// Copy-on-write sharing: fork, then appends into shared and private blocks.
+static void test_cow() {
+  BlockPool pool(8, 256);
+  Sequence parent(iota(0, 300));
+  pool.allocate(parent, 0);  // blocks 0, 1
+  CHECK(parent.block_table.size() == 2 && pool.num_free_blocks() == 6);
+  Sequence child;
+  pool.fork(parent, child);
+  CHECK(child.block_table == parent.block_table && child.num_tokens == 300);
+  CHECK(pool.block(parent.block_table[0]).ref_count == 2 && pool.block(parent.block_table[1]).ref_count == 2);
+  CHECK(pool.num_free_blocks() == 6);
+  CHECK(throws([&] { pool.fork(parent, child); }));  // child already has a table
+  // Parent appends token 300 into the shared partial block 1: private copy.
+  const std::size_t shared = parent.block_table[1];
+  parent.append_token(1000);
+  CHECK(pool.can_append_cow(parent));
+  const auto cp = pool.may_append_cow(parent);
+  CHECK(cp.has_value() && cp->first == shared && cp->second != shared);
+  CHECK(parent.block_table[1] == cp->second && child.block_table[1] == shared);
+  CHECK(pool.block(shared).ref_count == 1 && pool.block(cp->second).ref_count == 1);
+  CHECK(pool.num_free_blocks() == 5);
+  // Child's block is now private: no copy.  Block 0 stays shared (full, never written).
+  child.append_token(2000);
+  CHECK(!pool.may_append_cow(child).has_value());
+  CHECK(pool.block(parent.block_table[0]).ref_count == 2);
+  // A token that starts a block gets a fresh one, no copy.
+  Sequence s2(iota(0, 256));
+  pool.allocate(s2, 0);
+  s2.append_token(7);
+  CHECK(s2.num_tokens % 256 == 1);
+  CHECK(!pool.may_append_cow(s2).has_value() && s2.block_table.size() == 2);
+  // No free block: can_append_cow refuses a copy.
+  BlockPool tiny(1, 256);
+  Sequence a(iota(0, 10));
+  tiny.allocate(a, 0);
+  Sequence b;
+  tiny.fork(a, b);
+  b.append_token(1);
+  CHECK(!tiny.can_append_cow(b));
+  CHECK(throws([&] { tiny.may_append_cow(b); }));
+  // Release everything: every block returns to the free list exactly once.
+  pool.deallocate(parent);
+  pool.deallocate(child);
+  pool.deallocate(s2);
+  CHECK(pool.num_free_blocks() == 8);
+}
+
 static uint16_t f2bf(float f) {
   uint32_t u;
   std::memcpy(&u, &f, 4);
@@ -275,6 +322,30 @@ static void test_gpu_append_known_answer() {
 
 // attention/mod.rs:277-323 flash_attn_decode_runs (ctx 32, 4 heads, 4 kv heads,
 // D 64): through DecodeStep, checked against an in-test fp64 softmax.
+// Copy-on-write copies in every layer with one launch (copy_blocks_all_layers).
+static void test_gpu_cow_all_layers() {
+  const std::size_t L = 3, NB = 4, BS = 16, H = 2, D = 64;
+  PagedKVCache cache(L, NB, BS, H, D, OXIDE_DTYPE_BF16);
+  const std::size_t blk = BS * H * D, half = L * NB * blk;
+  std::vector<uint16_t> host(2 * half);
+  for (std::size_t i = 0; i < host.size(); ++i) host[i] = static_cast<uint16_t>(i * 2654435761u >> 16);
+  void* base = cache.k_cache(0);
+  (void)hipMemcpy(base, host.data(), host.size() * 2, hipMemcpyHostToDevice);
+  cache.copy_blocks_all_layers({{1, 2}, {3, 0}}, nullptr);
+  (void)hipDeviceSynchronize();
+  std::vector<uint16_t> got(host.size());
+  (void)hipMemcpy(got.data(), base, got.size() * 2, hipMemcpyDeviceToHost);
+  std::vector<uint16_t> want = host;
+  for (std::size_t kv = 0; kv < 2; ++kv)
+    for (std::size_t l = 0; l < L; ++l) {
+      const std::size_t off = kv * half + l * NB * blk;
+      std::memcpy(&want[off + 2 * blk], &host[off + 1 * blk], blk * 2);
+      std::memcpy(&want[off + 0 * blk], &host[off + 3 * blk], blk * 2);
+    }
+  CHECK(got == want);
+  CHECK(throws([&] { cache.copy_blocks_all_layers({{1, 4}}, nullptr); }));
+}
+
 static void test_gpu_decode_step() {
   const std::size_t Hq = 4, H = 4, D = 64, ctx = 32;
   PagedKVCache cache(2, 1, 256, H, D, OXIDE_DTYPE_BF16);
@@ -360,8 +431,10 @@ int main(int argc, char** argv) {
     test_metadata();
     test_slot_mapping();
     test_block_pool();
+    test_cow();
   } else if (mode == "gpu") {
     test_gpu_append_known_answer();
+    test_gpu_cow_all_layers();
     test_gpu_decode_step();
   } else {
     std::printf("usage: test_host cpu|gpu|hash <seed> <hex>\n");

@@ -136,6 +136,43 @@ void BlockPool::may_append(Sequence& seq) {
   if (seq.num_tokens % block_size_ == 1) seq.block_table.push_back(allocate_block());
 }
 
+void BlockPool::fork(const Sequence& parent, Sequence& child) {
+  if (!child.block_table.empty()) throw BlockPoolError("sequence already has a block table");
+  for (std::size_t id : parent.block_table) {
+    if (!used_block_ids_.count(id)) throw BlockPoolError("block " + std::to_string(id) + " is not in use");
+    ++blocks_[id].ref_count;
+  }
+  child.token_ids = parent.token_ids;
+  child.num_tokens = parent.num_tokens;
+  child.num_cached_tokens = parent.num_cached_tokens;
+  child.num_scheduled_tokens = 0;
+  child.block_table = parent.block_table;
+}
+
+bool BlockPool::can_append_cow(const Sequence& seq) const {
+  std::size_t need = 0;
+  if (seq.num_tokens % block_size_ == 1) {
+    need = 1;
+  } else if (!seq.block_table.empty() && blocks_[seq.block_table.back()].ref_count > 1) {
+    need = 1;
+  }
+  return free_block_ids_.size() >= need;
+}
+
+std::optional<std::pair<std::size_t, std::size_t>> BlockPool::may_append_cow(Sequence& seq) {
+  if (seq.num_tokens % block_size_ == 1) {
+    seq.block_table.push_back(allocate_block());
+    return std::nullopt;
+  }
+  if (seq.block_table.empty()) return std::nullopt;
+  const std::size_t src = seq.block_table.back();
+  if (blocks_[src].ref_count <= 1) return std::nullopt;
+  const std::size_t dst = allocate_block();
+  --blocks_[src].ref_count;
+  seq.block_table.back() = dst;
+  return std::make_pair(src, dst);
+}
+
 void BlockPool::register_hash(std::size_t id, int64_t h, std::vector<uint32_t> tokens) {
   blocks_.at(id).hash = h;
   blocks_[id].token_ids = std::move(tokens);

@@ -25,6 +25,7 @@
 #include <string>
 #include <unordered_map>
 #include <unordered_set>
+#include <utility>
 #include <vector>
 
 namespace oxide::host {
@@ -117,6 +118,22 @@ class BlockPool {
   void may_append(Sequence& seq);  // new block iff num_tokens % block_size == 1
   void hash_blocks(Sequence& seq);
 
+  // Copy-on-write sharing of whole block tables (parallel sampling, beam
+  // search).  The reference's pool shares only full, hashed prefix blocks, so
+  // it never writes into a shared block (its copy_blocks kernel has no
+  // caller); these three calls add the missing write path.
+  //   fork: `child` takes `parent`'s tokens and block table; every block gains
+  //         a reference.
+  //   can_append_cow / may_append_cow: call after appending a token to `seq`
+  //         (num_tokens counts it).  A token that starts a block gets a fresh
+  //         block (may_append); a token that lands in a block other tables
+  //         still reference gets a private copy of it: the returned
+  //         (src, dst) pair must be copied in the cache (copy_blocks) before the
+  //         token's K/V are written.
+  void fork(const Sequence& parent, Sequence& child);
+  bool can_append_cow(const Sequence& seq) const;
+  std::optional<std::pair<std::size_t, std::size_t>> may_append_cow(Sequence& seq);
+
   std::size_t num_free_blocks() const { return free_block_ids_.size(); }
   std::size_t num_blocks() const { return blocks_.size(); }
   std::size_t block_size() const { return block_size_; }
@@ -146,6 +163,11 @@ class KvCacheManager {
   bool can_append(const Sequence& s) const { return pool_.can_append(s); }
   void may_append(Sequence& s) { pool_.may_append(s); }
   void hash_blocks(Sequence& s) { pool_.hash_blocks(s); }
+  void fork(const Sequence& parent, Sequence& child) { pool_.fork(parent, child); }
+  bool can_append_cow(const Sequence& s) const { return pool_.can_append_cow(s); }
+  std::optional<std::pair<std::size_t, std::size_t>> may_append_cow(Sequence& s) {
+    return pool_.may_append_cow(s);
+  }
   std::size_t num_free_blocks() const { return pool_.num_free_blocks(); }
   std::size_t block_size() const { return block_size_; }
   BlockPool& pool() { return pool_; }

@@ -36,6 +36,7 @@ PagedKVCache::PagedKVCache(std::size_t num_layers, std::size_t num_blocks, std::
 
 PagedKVCache::~PagedKVCache() {
   if (buffer_) (void)hipFree(buffer_);
+  if (d_map_) (void)hipFree(d_map_);
 }
 
 std::size_t PagedKVCache::elem_bytes() const {
@@ -72,6 +73,33 @@ void PagedKVCache::copy_blocks(std::size_t layer, const int64_t* block_mapping,
   ::copy_blocks(k_cache(layer), v_cache(layer), block_mapping, static_cast<int64_t>(num_pairs),
                 static_cast<int64_t>(block_size_ * num_kv_heads_ * head_dim_), dtype_, stream);
   check_lib("copy_blocks");
+}
+
+void PagedKVCache::copy_blocks_all_layers(const std::vector<std::pair<std::size_t, std::size_t>>& pairs,
+                                          hipStream_t stream) {
+  if (pairs.empty()) return;
+  for (const auto& pr : pairs)
+    if (pr.first >= num_blocks_ || pr.second >= num_blocks_) throw std::out_of_range("block id");
+  // The previous call's upload may still read the staging copy.
+  check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  h_map_.clear();
+  for (std::size_t l = 0; l < num_layers_; ++l)
+    for (const auto& pr : pairs) {
+      h_map_.push_back(static_cast<int64_t>(l * num_blocks_ + pr.first));
+      h_map_.push_back(static_cast<int64_t>(l * num_blocks_ + pr.second));
+    }
+  const std::size_t bytes = h_map_.size() * sizeof(int64_t);
+  if (bytes > cap_map_) {
+    if (d_map_) check(hipFree(d_map_), "hipFree");
+    d_map_ = nullptr;
+    check(hipMalloc(&d_map_, bytes), "hipMalloc(copy map)");
+    cap_map_ = bytes;
+  }
+  check(hipMemcpyAsync(d_map_, h_map_.data(), bytes, hipMemcpyHostToDevice, stream), "upload copy map");
+  ::copy_blocks(k_cache(0), v_cache(0), static_cast<const int64_t*>(d_map_),
+                static_cast<int64_t>(h_map_.size() / 2),
+                static_cast<int64_t>(block_size_ * num_kv_heads_ * head_dim_), dtype_, stream);
+  check_lib("copy_blocks (all layers)");
 }
 
 DecodeStep::DecodeStep(const PagedKVCache& cache, std::size_t num_heads)

@@ -47,11 +47,19 @@ class PagedKVCache {
   // block_mapping: device int64 [num_pairs, 2] (src, dst), applied to one layer.
   void copy_blocks(std::size_t layer, const int64_t* block_mapping, std::size_t num_pairs,
                    hipStream_t stream) const;
+  // Copy-on-write copies of a step (host (src, dst) block pairs, e.g. from
+  // KvCacheManager::may_append_cow) in every layer, K and V, with one launch:
+  // block b of layer l is block l * num_blocks + b of the buffer's K (V) half.
+  void copy_blocks_all_layers(const std::vector<std::pair<std::size_t, std::size_t>>& pairs,
+                              hipStream_t stream);
 
  private:
   std::size_t num_layers_, num_blocks_, block_size_, num_kv_heads_, head_dim_;
   int dtype_;
   void* buffer_ = nullptr;
+  std::vector<int64_t> h_map_;  // staging of copy_blocks_all_layers
+  void* d_map_ = nullptr;
+  std::size_t cap_map_ = 0;
 };
 
 class DecodeStep {
