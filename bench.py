@@ -205,6 +205,96 @@ def prefill_main(args) -> int:
     return 0
 
 
+def prologue_bytes(tokens: int, hq: int, hkv: int, d: int) -> int:
+    """HBM bytes of one qk_norm_rope_and_cache call: the qkv rows read, q written, k and v
+    written to their slots, one fp32 cos/sin row, the position and the slot per token
+    (the [D] norm weights stay in cache)."""
+    return tokens * ((hq + 2 * hkv) * d * 2 + hq * d * 2 + 2 * hkv * d * 2 + d * 4 + 4 + 8)
+
+
+def prologue_cpu_baseline(seed: int, min_seconds: float = 10.0) -> dict:
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(seed)
+    T, Hq, Hkv, D = 256, 32, 8, 128
+    qkv = oracle.f32_to_bf16_bits(rng.standard_normal(size=(T, (Hq + 2 * Hkv) * D), dtype=np.float32))
+    w = oracle.f32_to_bf16_bits(np.ones(D, np.float32))
+    cs = oracle.rope_cos_sin_cache(8192, D, 1_000_000.0)
+    pos = rng.integers(0, 8192, T).astype(np.int32)
+    kc = np.zeros((T, Hkv, D), np.uint16)
+    vc = np.zeros_like(kc)
+    slots = np.arange(T, dtype=np.int64)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        oracle.qk_norm_rope_and_cache(qkv, Hq, Hkv, D, w, w, 1e-6, cs, pos, kc, vc, slots)
+        reps += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_seconds:
+            break
+    return {"value": round(prologue_bytes(T, Hq, Hkv, D) * reps / dt / 1e9, 4), "unit": "GB/s", "cores": 1,
+            "kind": "port", "sample": f"{T} tokens, Qwen3-8B heads, scalar C, {reps} reps in {dt:.1f} s"}
+
+
+def prologue_main(args) -> int:
+    import torch
+
+    import oxide_paged_kv as ox
+
+    dev = torch.device("cuda:0")
+    T, Hq, Hkv, D, BS = args.tokens, 32, 8, 128, 256
+    layers = 4
+    g = torch.Generator(device=dev).manual_seed(args.seed)
+    qkv = torch.randn((layers, T, (Hq + 2 * Hkv) * D), generator=g, device=dev).bfloat16()
+    w = (1 + 0.1 * torch.randn((2, D), generator=g, device=dev)).bfloat16()
+    cs = ox.rope_cos_sin_cache(32768, D, 1_000_000.0, dev)
+    # Prefill-sized calls: prompts of 4096 tokens at positions 0..4095; decode-sized
+    # calls (<= 256 tokens, one per sequence): scattered positions.
+    if T > 256:
+        pos = (torch.arange(T, device=dev, dtype=torch.int32) % 4096).contiguous()
+    else:
+        pos = torch.randint(0, 32768, (T,), generator=g, device=dev, dtype=torch.int32)
+    nb = (T + BS - 1) // BS
+    kc = torch.zeros((nb, BS, Hkv, D), dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    slots = torch.randperm(nb * BS, generator=g, device=dev)[:T].contiguous()
+
+    def call(i):
+        ox.qk_norm_rope_and_cache(qkv[i % layers], Hq, Hkv, w[0], w[1], 1e-6, cs, pos, kc, vc, slots)
+
+    for i in range(args.warmup):
+        call(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(args.steps):
+        call(i)
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us = e0.elapsed_time(e1) / args.steps * 1e3
+    nbytes = prologue_bytes(T, Hq, Hkv, D)
+    gbps = nbytes / (us * 1e-6) / 1e9
+    res = {
+        "metric": "fused q/k RMSNorm + RoPE + KV append GB/s (Qwen3-8B heads)",
+        "value": round(gbps, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1) qkv rows, random slots; positions 0..4095 per prompt (T > 256) or random",
+        "config": {"workload": f"prologue-qwen3-8b-{T}tok", "tokens": T, "num_heads": Hq, "num_kv_heads": Hkv,
+                   "head_dim": D},
+        "call_us": round(us, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "qk_norm_rope_cache_kernel", "algorithmic_bytes": nbytes},
+    }
+    if not args.no_cpu_baseline:
+        res["cpu_baseline"] = prologue_cpu_baseline(args.seed)
+    print(json.dumps(res), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -221,6 +311,9 @@ def main() -> int:
     ap.add_argument("--prompts", type=int, default=4, help="--prefill: prompts per call")
     ap.add_argument("--prompt-len", type=int, default=4096, help="--prefill: new tokens per prompt")
     ap.add_argument("--prefix", type=int, default=0, help="--prefill: cached tokens before each prompt")
+    ap.add_argument("--prologue", action="store_true",
+                    help="time the fused q/k norm + RoPE + KV append instead of the decode step")
+    ap.add_argument("--tokens", type=int, default=16384, help="--prologue: tokens per call")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -228,6 +321,8 @@ def main() -> int:
         return 2
     if args.prefill:
         return prefill_main(args)
+    if args.prologue:
+        return prologue_main(args)
 
     import numpy as np
     import torch

@@ -18,11 +18,15 @@
 // square root are correctly rounded.  The mean of squares is a tree sum, so it
 // can differ from another backend's order in the last fp32 bit.
 //
-// One workgroup (256 lanes) per token.  A head is handled by 16 lanes: lane i
-// holds elements [e i, e i + e) of each half (e = D / 32), i.e. the rotation
-// partners x1[j] and x2[j] sit in the same lane.  16 heads per pass over the
-// Hq + Hkv q and k heads; the v row is copied bitwise in 16-byte pieces.
+// Work split: a task is one head of one token -- a q head, a k head (norm +
+// rotation) or a v head (copy) -- handled by D / 16 lanes (8 at D = 128);
+// tasks are numbered token-major and spread over a grid-stride loop.  Lane i
+// of a q/k task holds elements [8 i, 8 i + 8) of each half, so the rotation
+// partners x1[j] and x2[j] sit in the same lane and every access is 16 bytes
+// (per element when a row is not 16-byte aligned).
 #include <math.h>
+
+#include <algorithm>
 
 #include "cdna4_tile.hpp"
 #include "oxide_common.hpp"
@@ -30,7 +34,8 @@
 namespace {
 
 constexpr int kRopeThreads = 256;
-constexpr int kLanesPerHead = 16;
+template <int D>
+constexpr int kLanesPerHead = D / 16;  // 8 elements of each half per lane
 
 __device__ __forceinline__ float to_f32(Bf16Tag, uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 __device__ __forceinline__ float to_f32(F16Tag, uint16_t h) {
@@ -56,25 +61,80 @@ struct RopeParams {
   int max_position;
   int num_heads;
   int num_kv_heads;
+  int64_t num_tokens;
   float eps;
-  bool vec_v;  // v row and cache rows 16-byte aligned
+  bool vec;  // every row and head slice 8-byte aligned: vector loads and stores
 };
+
+typedef uint4 vec_t;  // 8 16-bit values
+constexpr int E = 8;   // elements of each half per lane
+
+template <class Tag, int D>
+__device__ __forceinline__ void rope_task(const RopeParams& p, int64_t task, int heads);
 
 template <class Tag, int D>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_cache_kernel(RopeParams p) {
+  const int heads = p.num_heads + 2 * p.num_kv_heads;  // q, k, v heads per token
+  constexpr int kTasksPerWg = kRopeThreads / kLanesPerHead<D>;
+  const int64_t tasks = p.num_tokens * heads;
+  for (int64_t task = static_cast<int64_t>(blockIdx.x) * kTasksPerWg + threadIdx.x / kLanesPerHead<D>;
+       task < tasks; task += static_cast<int64_t>(gridDim.x) * kTasksPerWg) {
+    rope_task<Tag, D>(p, task, heads);
+  }
+}
+
+template <class Tag, int D>
+__device__ __forceinline__ void rope_task(const RopeParams& p, int64_t task, int heads) {
   // Every product and sum is rounded on its own, as in the reference.
 #pragma clang fp contract(off)
-  constexpr int E = D / 2 / kLanesPerHead;  // elements per lane per half
-  const int64_t t = blockIdx.x;
-  const int sub = threadIdx.x % kLanesPerHead;
-  const int slot_in_pass = threadIdx.x / kLanesPerHead;
+  constexpr int LPH = kLanesPerHead<D>;
+  const int64_t t = task / heads;
+  const int h = static_cast<int>(task % heads);
+  const int sub = threadIdx.x % LPH;
+  const uint16_t* src = p.qkv + t * p.qkv_stride + static_cast<int64_t>(h) * D;
+  const int64_t slot = p.slot_mapping ? p.slot_mapping[t] : -1;
+
+  if (h >= p.num_heads + p.num_kv_heads) {
+    // v head: bitwise copy into the slot (2 x 16 bytes per lane).
+    if (slot < 0) return;
+    uint16_t* dst = p.value_cache + (slot * p.num_kv_heads + (h - p.num_heads - p.num_kv_heads)) * D;
+    if (p.vec) {
+      *reinterpret_cast<vec_t*>(dst + sub * E) = *reinterpret_cast<const vec_t*>(src + sub * E);
+      *reinterpret_cast<vec_t*>(dst + D / 2 + sub * E) = *reinterpret_cast<const vec_t*>(src + D / 2 + sub * E);
+    } else {
+#pragma unroll
+      for (int i = sub; i < D; i += LPH) dst[i] = src[i];
+    }
+    return;
+  }
+
+  // Inputs first (independent loads), then the position-dependent cos / sin.
+  uint16_t r1[E], r2[E];
+  if (p.vec) {
+    const vec_t a = *reinterpret_cast<const vec_t*>(src + sub * E);
+    const vec_t b = *reinterpret_cast<const vec_t*>(src + D / 2 + sub * E);
+    __builtin_memcpy(r1, &a, sizeof(a));
+    __builtin_memcpy(r2, &b, sizeof(b));
+  } else {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      r1[e] = src[sub * E + e];
+      r2[e] = src[D / 2 + sub * E + e];
+    }
+  }
+  const bool is_q = h < p.num_heads;
+  const uint16_t* w = is_q ? p.q_weight : p.k_weight;
+  uint16_t w1[E], w2[E];
+  if (w != nullptr) {
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      w1[e] = w[sub * E + e];
+      w2[e] = w[D / 2 + sub * E + e];
+    }
+  }
   int pos = p.positions[t];
   pos = min(max(pos, 0), p.max_position - 1);
   const float* cs = p.cos_sin + static_cast<int64_t>(pos) * D;
-  const uint16_t* row = p.qkv + t * p.qkv_stride;
-  const int64_t slot = p.slot_mapping ? p.slot_mapping[t] : -1;
-  const int heads = p.num_heads + p.num_kv_heads;
-
   float c[E], s[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
@@ -82,74 +142,64 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_cache_kernel(RopePa
     s[e] = cs[D / 2 + sub * E + e];
   }
 
-  for (int h = slot_in_pass; h < heads; h += kRopeThreads / kLanesPerHead) {
-    const bool is_q = h < p.num_heads;
-    const uint16_t* src = row + static_cast<int64_t>(h) * D;
-    float x1[E], x2[E];
+  float x1[E], x2[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    x1[e] = to_f32(Tag{}, r1[e]);
+    x2[e] = to_f32(Tag{}, r2[e]);
+  }
+  if (w != nullptr) {
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < E; ++e) ss = ss + (x1[e] * x1[e] + x2[e] * x2[e]);
+#pragma unroll
+    for (int m = 1; m < LPH; m <<= 1) ss = ss + __shfl_xor(ss, m);
+    const float sd = sqrtf(ss / static_cast<float>(D) + p.eps);  // correctly rounded / and sqrt
 #pragma unroll
     for (int e = 0; e < E; ++e) {
-      x1[e] = to_f32(Tag{}, src[sub * E + e]);
-      x2[e] = to_f32(Tag{}, src[D / 2 + sub * E + e]);
-    }
-    const uint16_t* w = is_q ? p.q_weight : p.k_weight;
-    if (w != nullptr) {
-      float ss = 0.f;
-#pragma unroll
-      for (int e = 0; e < E; ++e) ss = ss + (x1[e] * x1[e] + x2[e] * x2[e]);
-#pragma unroll
-      for (int m = 1; m < kLanesPerHead; m <<= 1) ss = ss + __shfl_xor(ss, m);
-      const float sd = sqrtf(ss / static_cast<float>(D) + p.eps);  // correctly rounded / and sqrt
-#pragma unroll
-      for (int e = 0; e < E; ++e) {
-        x1[e] = round_to<Tag>(round_to<Tag>(x1[e] / sd) * to_f32(Tag{}, w[sub * E + e]));
-        x2[e] = round_to<Tag>(round_to<Tag>(x2[e] / sd) * to_f32(Tag{}, w[D / 2 + sub * E + e]));
-      }
-    }
-    uint16_t y1[E], y2[E];
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      y1[e] = pack1(Tag{}, x1[e] * c[e] - x2[e] * s[e]);
-      y2[e] = pack1(Tag{}, x2[e] * c[e] + x1[e] * s[e]);
-    }
-    uint16_t* dst0;
-    uint16_t* dst1 = nullptr;
-    if (is_q) {
-      dst0 = p.q_out + (t * p.num_heads + h) * D;
-    } else {
-      const int kh = h - p.num_heads;
-      dst0 = p.k_out ? p.k_out + (t * p.num_kv_heads + kh) * D : nullptr;
-      dst1 = slot >= 0 ? p.key_cache + (slot * p.num_kv_heads + kh) * D : nullptr;
-    }
-#pragma unroll
-    for (int e = 0; e < E; ++e) {
-      if (dst0) {
-        dst0[sub * E + e] = y1[e];
-        dst0[D / 2 + sub * E + e] = y2[e];
-      }
-      if (dst1) {
-        dst1[sub * E + e] = y1[e];
-        dst1[D / 2 + sub * E + e] = y2[e];
-      }
+      x1[e] = round_to<Tag>(round_to<Tag>(x1[e] / sd) * to_f32(Tag{}, w1[e]));
+      x2[e] = round_to<Tag>(round_to<Tag>(x2[e] / sd) * to_f32(Tag{}, w2[e]));
     }
   }
-
-  // v: bitwise copy of the row's last Hkv * D elements into the slot.
-  if (slot >= 0) {
-    const uint16_t* vsrc = row + static_cast<int64_t>(heads) * D;
-    uint16_t* vdst = p.value_cache + slot * p.num_kv_heads * D;
-    const int n = p.num_kv_heads * D;
-    if (p.vec_v) {
-      for (int i = threadIdx.x; i < n / 8; i += kRopeThreads)
-        reinterpret_cast<uint4*>(vdst)[i] = reinterpret_cast<const uint4*>(vsrc)[i];
+  uint16_t y1[E], y2[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    y1[e] = pack1(Tag{}, x1[e] * c[e] - x2[e] * s[e]);
+    y2[e] = pack1(Tag{}, x2[e] * c[e] + x1[e] * s[e]);
+  }
+  uint16_t* dst0;
+  uint16_t* dst1 = nullptr;
+  if (is_q) {
+    dst0 = p.q_out + (t * p.num_heads + h) * D;
+  } else {
+    const int kh = h - p.num_heads;
+    dst0 = p.k_out ? p.k_out + (t * p.num_kv_heads + kh) * D : nullptr;
+    dst1 = slot >= 0 ? p.key_cache + (slot * p.num_kv_heads + kh) * D : nullptr;
+  }
+  for (uint16_t* dst : {dst0, dst1}) {
+    if (dst == nullptr) continue;
+    if (p.vec) {
+      vec_t a, b;
+      __builtin_memcpy(&a, y1, sizeof(a));
+      __builtin_memcpy(&b, y2, sizeof(b));
+      *reinterpret_cast<vec_t*>(dst + sub * E) = a;
+      *reinterpret_cast<vec_t*>(dst + D / 2 + sub * E) = b;
     } else {
-      for (int i = threadIdx.x; i < n; i += kRopeThreads) vdst[i] = vsrc[i];
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        dst[sub * E + e] = y1[e];
+        dst[D / 2 + sub * E + e] = y2[e];
+      }
     }
   }
 }
 
 template <class Tag>
 bool launch_rope(const RopeParams& p, int64_t num_tokens, int head_dim, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(num_tokens));
+  const int64_t tasks = num_tokens * (p.num_heads + 2 * p.num_kv_heads);
+  const int tpw = kRopeThreads / (static_cast<int>(head_dim) / 16);  // tasks per workgroup
+  const int64_t wgs = (tasks + tpw - 1) / tpw;
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(wgs, int64_t{1} << 20)));  // grid-stride beyond
   if (head_dim == 128) {
     hipLaunchKernelGGL((qk_norm_rope_cache_kernel<Tag, 128>), grid, dim3(kRopeThreads), 0, s, p);
     return true;
@@ -205,10 +255,12 @@ extern "C" void qk_norm_rope_and_cache(void* q_out, void* k_out, const void* qkv
   p.num_heads = static_cast<int>(num_heads);
   p.num_kv_heads = static_cast<int>(num_kv_heads);
   p.eps = static_cast<float>(eps);
-  // The v part of every row starts at (Hq + Hkv) * D elements; 16-byte copies
-  // need it, the row stride and the cache to be 16-byte aligned.
-  p.vec_v = oxide::aligned16(qkv) && oxide::aligned16(value_cache) && (qkv_row_stride * 2) % 16 == 0 &&
-            ((num_heads + num_kv_heads) * head_dim * 2) % 16 == 0 && (num_kv_heads * head_dim) % 8 == 0;
+  p.num_tokens = num_tokens;
+  // Head slices are D * 2 bytes apart (a multiple of 16); vector accesses need
+  // every base pointer and the qkv row stride 16-byte aligned as well.
+  auto al16 = [](const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; };
+  p.vec = al16(qkv) && al16(q_out) && al16(k_out) && al16(key_cache) && al16(value_cache) &&
+          (qkv_row_stride * 2) % 16 == 0;
   hipStream_t s = oxide::as_stream(stream);
   const bool ok = dtype == OXIDE_DTYPE_BF16 ? launch_rope<Bf16Tag>(p, num_tokens, static_cast<int>(head_dim), s)
                                             : launch_rope<F16Tag>(p, num_tokens, static_cast<int>(head_dim), s);
