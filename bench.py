@@ -441,6 +441,7 @@ def main() -> int:
                    "num_kv_heads": H, "head_dim": D, "block_size": BS, "pool_blocks": NB,
                    "ctx": [cfg.ctx_lo, cfg.ctx_hi], "window_left": cfg.window_left,
                    "layers_rotated": layers, "split_tokens": ox.split_tokens(cfg.batch, H, st.max_seqlen_k),
+                   "pass1": "split grid" if ox.split_tokens(cfg.batch, H, st.max_seqlen_k) else "persistent balanced",
                    "total_keys": int(st.context_lens.sum())},
         "step_mode": "separate append + attention" if args.separate else "fused append + attention (one launch)",
         "attn_us": round(attn_us, 2),

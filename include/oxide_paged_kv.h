@@ -161,9 +161,18 @@ size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
                                              int64_t num_kv_heads, int64_t head_dim,
                                              int64_t max_seqlen_k);
 
-/* Tokens per KV split chosen for these arguments (a multiple of 256). */
+/* Tokens per KV split chosen for these arguments (256, 512 or 1024), or 0
+ * when the balanced persistent pass is chosen instead: long contexts, where
+ * batch * max_seqlen_k * num_kv_heads reaches 16384 positions per resident
+ * workgroup (CUs x 2); it then splits the summed (sequence, kv head, key)
+ * positions evenly over one workgroup per resident slot. */
 int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
                                             int64_t max_seqlen_k);
+
+/* Process-wide override of that choice (no counterpart in the reference; for
+ * tuning and tests): 0 = by shape (default), 1 = always the split grid,
+ * 2 = always the persistent pass.  Results agree within rounding either way. */
+void oxide_set_decode_path(int path);
 
 /*
  * Prefill attention over the paged cache.  Replaces the general (seqlen_q >= 1)

@@ -64,12 +64,23 @@ CASES = [
 ]
 
 
+@pytest.fixture(params=[1, 2], ids=["split", "persistent"])
+def decode_path(request):
+    """Runs a test once per pass-1 path (split grid, persistent balanced pass)."""
+    import oxide_paged_kv as ox
+
+    ox.set_decode_path(request.param)
+    yield request.param
+    ox.set_decode_path(0)
+
+
 @pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
-def test_decode_vs_oracle(device, case):
+def test_decode_vs_oracle(device, case, decode_path):
     B, Hq, Hkv, D, BS, NB, lens, window, dtype = case
     q, kc, vc, cu, table, mx = _case(11, B, Hq, Hkv, D, BS, NB, lens, dtype)
     scale = 1.0 / math.sqrt(D)
-    print(f"decode case B={B} Hq={Hq} Hkv={Hkv} D={D} BS={BS} lens={lens} window={window} {dtype}", flush=True)
+    print(f"decode case B={B} Hq={Hq} Hkv={Hkv} D={D} BS={BS} lens={lens} window={window} {dtype} "
+          f"path={decode_path}", flush=True)
     got = to_f32(_run(device, q, kc, vc, cu, table, mx, scale, window, dtype))
     want = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype)
     assert_attn_close(got, want)
@@ -249,6 +260,44 @@ def test_decode_cfg4_prefix_cow_window_full_size(device):
     _check_sampled(st, kc, vc, q, out, [0, 37, 127], c.window_left)
 
 
+def test_decode_path_policy(device):
+    """Long contexts take the persistent balanced pass (split_tokens 0), the others a
+    split grid; cfg5 and cfg3 shapes."""
+    import oxide_paged_kv as ox
+
+    assert ox.split_tokens(16, 8, 131072) == 0
+    assert ox.split_tokens(64, 8, 8192) == 1024
+    ox.set_decode_path(1)
+    assert ox.split_tokens(16, 8, 131072) == 1024
+    ox.set_decode_path(2)
+    assert ox.split_tokens(64, 8, 8192) == 0
+    ox.set_decode_path(0)
+
+
+@pytest.mark.parametrize("cfg_id", [3, 5])
+def test_decode_paths_agree_full_size(device, cfg_id):
+    """Full-size cfg3 / cfg5 through both passes: outputs agree within rounding of
+    the partial merges (max-abs 2e-2, the attention tolerance)."""
+    import torch
+    import oxide_paged_kv as ox
+
+    st, kc, vc, q = _full_size_inputs(cfg_id, 70 + cfg_id, device)
+    c = st.cfg
+    cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
+    bt = torch.from_numpy(st.block_table).to(device)
+    outs = []
+    try:
+        for path in (1, 2):
+            ox.set_decode_path(path)
+            print(f"cfg{cfg_id} path {path}", flush=True)
+            outs.append(to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim))))
+    finally:
+        ox.set_decode_path(0)
+    assert_attn_close(outs[1], outs[0])
+    lens = st.context_lens.astype(np.int64)
+    _check_sampled(st, kc, vc, q, outs[1], [int(lens.argmax()), int(lens.argmin())])
+
+
 def test_decode_cfg5_long_context_full_size(device):
     """cfg5 at full size: Qwen3-32B decode shape (G = 8), 16 sequences of 32k-128k
     keys; the longest and the shortest sequences are checked against the oracle."""
@@ -299,7 +348,7 @@ FUSED_CASES = [
 
 
 @pytest.mark.parametrize("case", FUSED_CASES, ids=[f"f{i}" for i in range(len(FUSED_CASES))])
-def test_decode_fused_append_equals_append_then_attend(device, case):
+def test_decode_fused_append_equals_append_then_attend(device, case, decode_path):
     """paged_decode_attention_append == reshape_and_cache + paged_decode_attention,
     bit for bit (output and caches); slot -1 skips the append."""
     import torch

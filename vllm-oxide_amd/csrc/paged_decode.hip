@@ -39,6 +39,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <atomic>
 
 #include "cdna4_tile.hpp"
 #include "oxide_common.hpp"
@@ -60,6 +61,9 @@ namespace {
 #endif
 #ifndef OXIDE_GRID_MODE
 #define OXIDE_GRID_MODE 4  // workgroup -> (split, head, seq) order, see decode_work_item
+#endif
+#ifndef OXIDE_PERSIST_MAP
+#define OXIDE_PERSIST_MAP 1  // persistent range order: 0 = workgroup index, 1 = XCD-major
 #endif
 #ifndef OXIDE_KV_NONTEMPORAL
 #define OXIDE_KV_NONTEMPORAL 1  // 1 = K/V streamed with non-temporal loads
@@ -100,6 +104,7 @@ struct DecodeParams {
   int split_tokens;
   int max_splits;
   int batch;
+  int num_wgs;  // persistent path: workgroups sharing the flattened key space
   float scale_log2;
 };
 
@@ -169,63 +174,57 @@ __device__ __forceinline__ bool decode_work_item(const DecodeParams& p, int& spl
 // V rows in LDS are padded to D*2 + 32 bytes so the 4 rows one 16-lane group
 // reads land on disjoint banks.
 
+// Shared layout constants of pass 1.
+template <int D, int G, int TILES>
+struct SplitShape {
+  static constexpr int KK = D / 32;
+  static constexpr int CH = D / 8;
+  static constexpr int RPL = 64 / CH;
+  static constexpr int VL = 16 / RPL;
+  static constexpr int NDT = D / 16;          // 16-column output tiles
+  static constexpr int VRS = 2 * D + 32;      // padded V row in LDS (bytes)
+  static constexpr int WT = 16 * TILES;
+  static constexpr int KBYTES = 16 * CH * 16;                  // one K tile
+  static constexpr int WAVE_BYTES = KBYTES + 32 * VRS;         // K tile + 32 V rows
+  static constexpr int LOOP_BYTES = kWaves * WAVE_BYTES;
+  static constexpr int EPI_BYTES = kWaves * G * D * 4 + 2 * kWaves * G * 4;
+  static constexpr int SMEM = LOOP_BYTES > EPI_BYTES ? LOOP_BYTES : EPI_BYTES;
+};
+
+// The query rows of kv head kh (B operand of S^T; slot s holds query s % G).
+template <int D, int G>
+__device__ __forceinline__ void load_q(const DecodeParams& p, int b, int kh, uint4 (&qb)[D / 32]) {
+  const int lane = threadIdx.x & 63;
+  const uint16_t* qrow = static_cast<const uint16_t*>(p.q) +
+                         (static_cast<int64_t>(b) * p.num_heads + kh * G + (lane & 15) % G) * D;
+#pragma unroll
+  for (int kk = 0; kk < D / 32; ++kk) qb[kk] = *reinterpret_cast<const uint4*>(qrow + 8 * ((lane >> 4) + 4 * kk));
+}
+
+// One wave's pass over the TILES 16-key tiles from key w0, restricted to keys
+// [a, e) (a < e): updates the running max / partial sum of query slot lane % 16
+// and the PV accumulators.  L is the sequence length (the fused append owns key
+// L - 1).
 template <class Tag, int D, int G, int TILES>
-__global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_split(DecodeParams p) {
-  static_assert(TILES % 2 == 0, "PV steps take two 16-key tiles");
-  constexpr int KK = D / 32;
-  constexpr int CH = D / 8;
-  constexpr int RPL = 64 / CH;
-  constexpr int VL = 16 / RPL;
-  constexpr int NDT = D / 16;          // 16-column output tiles
-  constexpr int VRS = 2 * D + 32;      // padded V row in LDS (bytes)
-  constexpr int WT = 16 * TILES;
-  constexpr int KBYTES = 16 * CH * 16;                  // one K tile
-  constexpr int WAVE_BYTES = KBYTES + 32 * VRS;         // K tile + 32 V rows
-  constexpr int LOOP_BYTES = kWaves * WAVE_BYTES;
-  constexpr int EPI_BYTES = kWaves * G * D * 4 + 2 * kWaves * G * 4;
-  constexpr int SMEM = LOOP_BYTES > EPI_BYTES ? LOOP_BYTES : EPI_BYTES;
-  __shared__ __align__(16) char smem[SMEM];
-
-  int split, kh, b;
-  if (!decode_work_item(p, split, kh, b)) return;
-  const int L = seq_len(p, b);
-  const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
-  const int s0 = split * (kWaves * WT);
-  if (s0 >= L || s0 + kWaves * WT <= lo) return;
-
+__device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* smem, int b, int kh, int L,
+                                                  int w0, int a, int e, const uint4 (&qb)[D / 32],
+                                                  float& m_q, float& l_q, floatx4 (&acc)[D / 16]) {
+  typedef SplitShape<D, G, TILES> S;
+  constexpr int KK = S::KK, CH = S::CH, RPL = S::RPL, VL = S::VL, NDT = S::NDT, VRS = S::VRS;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int r16 = lane & 15;
   const int grp = lane >> 4;
   const int vch = lane % CH;
   const int vrow = lane / CH;
-  const int w0 = s0 + wave * WT;
-  const int a = __builtin_amdgcn_readfirstlane(max(lo, w0));
-  const int e = __builtin_amdgcn_readfirstlane(min(L, w0 + WT));
-
   const int BS = p.block_size;
   const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + kh * D;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + kh * D;
   const int32_t* bt = p.block_table + b * p.max_blocks;
-  const int qh0 = kh * G;
-
-  uint4* s_k = reinterpret_cast<uint4*>(smem + wave * WAVE_BYTES);  // [16][CH], swizzled
-  char* s_v = smem + wave * WAVE_BYTES + KBYTES;                    // [32][VRS]
-
-  float m_q = -INFINITY, l_q = 0.f;  // running max / this lane's partial sum, query slot r16
-  floatx4 acc[NDT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
-
-  if (a < e) {
-    const uint16_t* qrow = static_cast<const uint16_t*>(p.q) +
-                           (static_cast<int64_t>(b) * p.num_heads + qh0 + r16 % G) * D;
-    uint4 qb[KK];
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk)
-      qb[kk] = *reinterpret_cast<const uint4*>(qrow + 8 * (grp + 4 * kk));
-
+  uint4* s_k = reinterpret_cast<uint4*>(smem + wave * S::WAVE_BYTES);  // [16][CH], swizzled
+  char* s_v = smem + wave * S::WAVE_BYTES + S::KBYTES;                    // [32][VRS]
+  {
     const int first_tile = a & ~15;
     const int last_tile = (e - 1) & ~15;
     uint4 kst[2][VL], vst[2][VL];
@@ -351,6 +350,22 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
     }
   }
 
+}
+
+// Merges the 4 waves' states through LDS and writes, per query q of the group,
+// either the bf16/f16 output row (direct) or the normalised partial o and its
+// log2-sum-exp at partial row prow_base + q * prow_qstride.  Ends with a
+// barrier, so the LDS is free again on return.
+template <class Tag, int D, int G, int TILES>
+__device__ __forceinline__ void decode_epilogue(const DecodeParams& p, char* smem, int b, int kh, float m_q,
+                                                float l_q, const floatx4 (&acc)[D / 16], bool direct,
+                                                int64_t prow_base, int64_t prow_qstride) {
+  constexpr int NDT = D / 16;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int grp = lane >> 4;
+  const int qh0 = kh * G;
   // Wave totals: l summed over the 4 lane groups (every group then holds the
   // slot's total); maxima are already equal across groups.
   l_q += __shfl_xor(l_q, 16);
@@ -374,10 +389,7 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
   }
   __syncthreads();
 
-  const int first = lo / (kWaves * WT);
-  const int nsplits = (L - 1) / (kWaves * WT) - first + 1;
   uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + qh0) * D;
-  const int64_t prow0 = (static_cast<int64_t>(b) * p.num_heads + qh0) * p.max_splits;
   for (int idx = threadIdx.x; idx < G * D; idx += kThreads) {
     const int q = idx / D;
     const int d = idx % D;
@@ -393,13 +405,137 @@ __global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_
       osum += f * s_o[(w * G + q) * D + d];
     }
     const float o = lsum > 0.f ? osum / lsum : 0.f;
-    if (nsplits == 1) {
+    if (direct) {
       out[idx] = pack1(Tag{}, o);
     } else {
-      const int64_t prow = prow0 + static_cast<int64_t>(q) * p.max_splits + split;
+      const int64_t prow = prow_base + static_cast<int64_t>(q) * prow_qstride;
       p.part_o[prow * D + d] = o;
       if (d == 0) p.part_lse[prow] = lsum > 0.f ? msafe + log2f(lsum) : -INFINITY;
     }
+  }
+  __syncthreads();
+}
+
+template <class Tag, int D, int G, int TILES>
+__global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_split(DecodeParams p) {
+  static_assert(TILES % 2 == 0, "PV steps take two 16-key tiles");
+  typedef SplitShape<D, G, TILES> S;
+  __shared__ __align__(16) char smem[S::SMEM];
+
+  int split, kh, b;
+  if (!decode_work_item(p, split, kh, b)) return;
+  const int L = seq_len(p, b);
+  const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
+  const int s0 = split * (kWaves * S::WT);
+  if (s0 >= L || s0 + kWaves * S::WT <= lo) return;
+
+  const int wave = threadIdx.x >> 6;
+  const int w0 = s0 + wave * S::WT;
+  const int a = __builtin_amdgcn_readfirstlane(max(lo, w0));
+  const int e = __builtin_amdgcn_readfirstlane(min(L, w0 + S::WT));
+
+  float m_q = -INFINITY, l_q = 0.f;  // running max / this lane's partial sum, query slot lane % 16
+  floatx4 acc[S::NDT];
+#pragma unroll
+  for (int dt = 0; dt < S::NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  if (a < e) {
+    uint4 qb[S::KK];
+    load_q<D, G>(p, b, kh, qb);
+    decode_wave_tiles<Tag, D, G, TILES>(p, smem, b, kh, L, w0, a, e, qb, m_q, l_q, acc);
+  }
+  const int first = lo / (kWaves * S::WT);
+  const int nsplits = (L - 1) / (kWaves * S::WT) - first + 1;
+  const int64_t prow0 = (static_cast<int64_t>(b) * p.num_heads + kh * G) * p.max_splits;
+  decode_epilogue<Tag, D, G, TILES>(p, smem, b, kh, m_q, l_q, acc, nsplits == 1, prow0 + split, p.max_splits);
+}
+
+// ---------------------------------------------------------------------------
+// Balanced pass 1 (persistent): the (sequence, kv head, key) positions are
+// laid end to end -- position Hkv * cu_seqlens_k[b] + kh * L_b + j -- and
+// workgroup w of W takes positions [w N / W, (w+1) N / W), N = Hkv *
+// cu_seqlens_k[batch], so every workgroup streams the same number of K/V rows
+// whatever the spread of lengths.  Its range is cut into segments at (b, kh)
+// boundaries; per segment the 4 waves take 256-key blocks in turn (aligned to
+// 16 keys, masked to the segment), and the 4 waves' states merge in LDS.  A
+// segment that is a whole (b, kh) writes the output; a piece of a (b, kh) that
+// crosses workgroups writes a partial to slot (w, 0) if it is the workgroup's
+// first segment, else (w, 1) -- at most one of each per workgroup -- and pass 2
+// combines the pieces of each (b, kh) from the owners of its first and last
+// positions.
+__device__ __forceinline__ int64_t owner_wg(int64_t x, int64_t n, int w) {
+  return ((x + 1) * w - 1) / n;  // largest v with v * n / w <= x
+}
+
+// Largest b in [0, batch) with cu[b] <= key (cu non-decreasing).
+__device__ __forceinline__ int find_seq(const uint32_t* cu, int batch, int64_t key) {
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (static_cast<int64_t>(cu[mid]) <= key)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+template <class Tag, int D, int G>
+__global__ __launch_bounds__(kThreads, 2) void paged_decode_persistent(DecodeParams p) {
+  constexpr int TILES = 16;
+  typedef SplitShape<D, G, TILES> S;
+  __shared__ __align__(16) char smem[S::SMEM];
+  const int W = gridDim.x;
+#if OXIDE_PERSIST_MAP == 1
+  // Workgroup i runs on XCD i % 8: give each XCD a contiguous eighth of the
+  // ranges, so the pieces of one sequence stay in one L2 (W is a multiple of 8).
+  const int w = (blockIdx.x % kXcds) * (W / kXcds) + blockIdx.x / kXcds;
+#else
+  const int w = blockIdx.x;
+#endif
+  const int Hkv = p.num_kv_heads;
+  const int64_t N = static_cast<int64_t>(Hkv) * p.cu_seqlens_k[p.batch];
+  const int64_t R0 = static_cast<int64_t>(w) * N / W;
+  const int64_t R1 = static_cast<int64_t>(w + 1) * N / W;
+  if (R0 >= R1) return;
+  const int wave = threadIdx.x >> 6;
+  int b = find_seq(p.cu_seqlens_k, p.batch, R0 / Hkv);
+  int64_t x = R0;
+  while (x < R1 && b < p.batch) {
+    const int64_t cb = p.cu_seqlens_k[b];
+    const int64_t Lraw = max(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - cb, int64_t{0});
+    const int64_t base = static_cast<int64_t>(Hkv) * cb;
+    if (x < base) x = base;  // only with a decreasing cu_seqlens_k
+    if (x >= base + Hkv * Lraw) {
+      ++b;
+      continue;
+    }
+    const int kh = static_cast<int>((x - base) / Lraw);
+    const int64_t g0 = base + kh * Lraw;
+    const int64_t seg_end = min(R1, g0 + Lraw);
+    const int j0 = static_cast<int>(x - g0);
+    const int j1 = static_cast<int>(seg_end - g0);
+    const int L = seq_len(p, b);
+    const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
+    const int a_seg = max(j0, lo);
+    const int e_seg = min(j1, L);
+    float m_q = -INFINITY, l_q = 0.f;
+    floatx4 acc[S::NDT];
+#pragma unroll
+    for (int dt = 0; dt < S::NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (a_seg < e_seg) {
+      uint4 qb[S::KK];
+      load_q<D, G>(p, b, kh, qb);
+      for (int blk0 = (a_seg & ~15) + wave * S::WT; blk0 < e_seg; blk0 += kWaves * S::WT) {
+        const int a = max(a_seg, blk0);
+        const int e = min(e_seg, blk0 + S::WT);
+        decode_wave_tiles<Tag, D, G, TILES>(p, smem, b, kh, L, blk0, a, e, qb, m_q, l_q, acc);
+      }
+    }
+    const bool direct = j0 == 0 && j1 == Lraw;
+    const int slot = x == R0 ? 0 : 1;
+    decode_epilogue<Tag, D, G, TILES>(p, smem, b, kh, m_q, l_q, acc, direct,
+                                      (static_cast<int64_t>(w) * 2 + slot) * G, 1);
+    x = seg_end;
   }
 }
 
@@ -506,6 +642,120 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge(DecodeParams p) {
   }
 }
 
+// Pass 2 of the persistent path: per (query head, sequence), the pieces of
+// its (b, kh) from workgroups owner(g0) .. owner(g0 + L - 1), combined with
+// log-sum-exp weights (a piece outside the window has weight 0).
+template <class Tag, int D>
+__global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(DecodeParams p) {
+  constexpr int PER = D / 64;
+  __shared__ float s_o[kWaves][D];
+  __shared__ float s_mw[kWaves][2];
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int G = p.num_heads / p.num_kv_heads;
+  const int kh = h / G;
+  const int q = h % G;
+  const int64_t cb = p.cu_seqlens_k[b];
+  const int64_t Lraw = max(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - cb, int64_t{0});
+  uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + h) * D;
+  if (Lraw == 0 || seq_len(p, b) == 0) {
+    for (int i = threadIdx.x; i < D; i += kThreads) out[i] = 0;
+    // Fused append of a sequence with no keys to attend to: the first query
+    // head of each kv-head group writes that head's slice of the new row.
+    if (p.new_k != nullptr && q == 0) {
+      const int64_t slot = p.slot_mapping[b];
+      const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
+      const int64_t src = (static_cast<int64_t>(b) * p.num_kv_heads + kh) * D;
+      for (int i = threadIdx.x; slot >= 0 && i < D; i += kThreads) {
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.k))[slot * row_stride + kh * D + i] =
+            static_cast<const uint16_t*>(p.new_k)[src + i];
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.v))[slot * row_stride + kh * D + i] =
+            static_cast<const uint16_t*>(p.new_v)[src + i];
+      }
+    }
+    return;
+  }
+  const int W = p.num_wgs;
+  const int64_t N = static_cast<int64_t>(p.num_kv_heads) * p.cu_seqlens_k[p.batch];
+  const int64_t g0 = static_cast<int64_t>(p.num_kv_heads) * cb + kh * Lraw;
+  if (g0 + Lraw > N) {  // inconsistent cu_seqlens_k: pass 1 did not cover these keys
+    for (int i = threadIdx.x; i < D; i += kThreads) out[i] = 0;
+    return;
+  }
+  const int64_t wa = owner_wg(g0, N, W);
+  const int64_t wb = owner_wg(g0 + Lraw - 1, N, W);
+  if (wa == wb) return;  // one workgroup held all of it and wrote the output
+  const int s_first = wa * N / W < g0 ? 1 : 0;
+  auto row = [&](int i) -> int64_t { return ((wa + i) * 2 + (i == 0 ? s_first : 0)) * G + q; };
+  // With fewer positions than workgroups some own an empty range and wrote
+  // nothing: their slots are skipped.
+  auto piece_lse = [&](int i) -> float {
+    const int64_t v = wa + i;
+    return v * N / W < (v + 1) * N / W ? p.part_lse[row(i)] : -INFINITY;
+  };
+  const int n = static_cast<int>(wb - wa + 1);
+  const int chunk = (n + kWaves - 1) / kWaves;
+  const int w_first = wave * chunk;
+  const int w_last = min(n - 1, w_first + chunk - 1);
+
+  float M = -INFINITY;
+  for (int i = w_first + lane; i <= w_last; i += 64) M = fmaxf(M, piece_lse(i));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
+  const float msafe = M == -INFINITY ? 0.f : M;
+  float o[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) o[i] = 0.f;
+  float wsum = 0.f;
+  for (int g = w_first; g <= w_last; g += 64) {
+    const int cnt = min(64, w_last - g + 1);
+    const float lse = lane < cnt ? piece_lse(g + lane) : -INFINITY;
+    const float wl = lane < cnt && lse != -INFINITY ? __builtin_amdgcn_exp2f(lse - msafe) : 0.f;
+    float ws = wl;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ws += __shfl_xor(ws, m);
+    wsum += ws;
+    for (int i = 0; i < cnt; ++i) {
+      const float wi =
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i));
+      if (wi == 0.f) continue;  // empty or fully windowed-out piece
+      const float* po = p.part_o + row(g + i) * D + lane;
+#pragma unroll
+      for (int k = 0; k < PER; ++k) o[k] = fmaf(wi, po[64 * k], o[k]);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < PER; ++k) s_o[wave][lane + 64 * k] = o[k];
+  if (lane == 0) {
+    s_mw[wave][0] = w_first <= w_last ? M : -INFINITY;
+    s_mw[wave][1] = wsum;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float Mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) Mt = fmaxf(Mt, s_mw[w][0]);
+    const float mt = Mt == -INFINITY ? 0.f : Mt;
+    float f[kWaves], wt = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = s_mw[w][0];
+      f[w] = mw == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(mw - mt);
+      wt += f[w] * s_mw[w][1];
+    }
+    const float inv = wt > 0.f ? 1.f / wt : 0.f;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) acc = fmaf(f[w], s_o[w][lane + 64 * k], acc);
+      out[lane + 64 * k] = pack1(Tag{}, acc * inv);
+    }
+  }
+}
+
 // Zero output for a batch whose max_seqlen_k is 0 (no split workgroups run).
 __global__ __launch_bounds__(256) void zero_fill_u16(uint16_t* out, int64_t n) {
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n;
@@ -514,6 +764,25 @@ __global__ __launch_bounds__(256) void zero_fill_u16(uint16_t* out, int64_t n) {
 }
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Pass-1 path: 1 = split grid (paged_decode_split), 2 = persistent balanced
+// (paged_decode_persistent); 0 = choose by shape.  Set by oxide_set_decode_path.
+std::atomic<int> g_decode_path{0};
+
+int device_cu_count();
+
+// The persistent path pays off when each of its workgroups streams a long
+// range: at most batch * max_seqlen_k * Hkv positions over CUs x 2 workgroups.
+// Measured on MI355X: faster from ~16 k positions per workgroup (Qwen3-32B
+// B=16 ctx 32k-128k: 883 vs 953 us); slower below (Qwen3-8B B=64 ctx 2k-8k,
+// Qwen3-0.6B B=32 ctx 0.5k-4k), where the split grid's many short workgroups
+// hide their start-up and the XCD-aware order helps more than the balance.
+bool use_persistent(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
+  const int forced = g_decode_path.load(std::memory_order_relaxed);
+  if (forced == 1) return false;
+  if (forced == 2) return true;
+  return batch * max_seqlen_k * num_kv_heads >= int64_t{16384} * 2 * device_cu_count();
+}
 
 int64_t choose_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
   // The longest split (fewest partials, shortest merge) that still yields at
@@ -569,6 +838,58 @@ bool dispatch_group(const DecodeParams& p, int64_t batch, int group, hipStream_t
   }
 }
 
+// Workgroups per CU of the persistent path, at most (bounds the workspace).
+constexpr int kMaxWgsPerCu = 4;
+constexpr int kMaxDevices = 64;
+
+int device_cu_count() {
+  static int cache[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  int& n = cache[dev % kMaxDevices];
+  if (n == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    n = v;
+  }
+  return n;
+}
+
+template <class Tag, int D, int G>
+void launch_persistent(DecodeParams p, hipStream_t s) {
+  // One workgroup per resident slot: CUs x the kernel's occupancy.
+  static int occ_cache[kMaxDevices] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  int& occ = occ_cache[dev % kMaxDevices];
+  if (occ == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_persistent<Tag, D, G>, kThreads, 0) !=
+        hipSuccess)
+      n = 2;
+    occ = std::max(1, std::min(n, kMaxWgsPerCu));
+  }
+  p.num_wgs = device_cu_count() * occ;
+  p.num_wgs -= p.num_wgs % kXcds;  // a whole number of workgroups per XCD
+  hipLaunchKernelGGL((paged_decode_persistent<Tag, D, G>), dim3(static_cast<unsigned>(p.num_wgs)),
+                     dim3(kThreads), 0, s, p);
+  hipLaunchKernelGGL((paged_decode_merge_persistent<Tag, D>),
+                     dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(kThreads),
+                     0, s, p);
+}
+
+template <class Tag, int D>
+bool dispatch_persistent(const DecodeParams& p, int group, hipStream_t s) {
+  switch (group) {
+    case 1: launch_persistent<Tag, D, 1>(p, s); return true;
+    case 2: launch_persistent<Tag, D, 2>(p, s); return true;
+    case 4: launch_persistent<Tag, D, 4>(p, s); return true;
+    case 8: launch_persistent<Tag, D, 8>(p, s); return true;
+    case 16: launch_persistent<Tag, D, 16>(p, s); return true;
+    default: return false;
+  }
+}
+
 template <class Tag>
 bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hipStream_t s) {
   if (p.max_splits == 0) {
@@ -577,6 +898,11 @@ bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hip
     hipLaunchKernelGGL(zero_fill_u16, dim3(static_cast<unsigned>(std::min<int64_t>((n + 255) / 256, 4096))),
                        dim3(256), 0, s, static_cast<uint16_t*>(p.out), n);
     return true;
+  }
+  if (p.split_tokens == 0) {
+    if (head_dim == 128) return dispatch_persistent<Tag, 128>(p, group, s);
+    if (head_dim == 64) return dispatch_persistent<Tag, 64>(p, group, s);
+    return false;
   }
   const dim3 mgrid(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(batch));
   if (head_dim == 128) {
@@ -592,26 +918,35 @@ bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hip
   return false;
 }
 
-// Workspace: part_o [B, Hq, splits, D] f32 | part_lse [B, Hq, splits] f32,
-// each 256-byte aligned.
+// Workspace: part_o [rows, D] f32 | part_lse [rows] f32, each 256-byte
+// aligned.  Split path: a row per (sequence, query head, split); persistent
+// path: two per workgroup and query of the group.
 struct WorkspaceLayout {
   int64_t lse_off, total;
 };
-WorkspaceLayout workspace_layout(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
-                                 int64_t head_dim, int64_t max_seqlen_k) {
-  const int64_t st = choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
-  const int64_t rows = batch * num_heads * ceil_div(max_seqlen_k, st);
+WorkspaceLayout workspace_layout(int64_t rows, int64_t head_dim) {
   WorkspaceLayout w;
   w.lse_off = ceil_div(rows * head_dim * 4, 256) * 256;
   w.total = w.lse_off + ceil_div(rows * 4, 256) * 256;
   return w;
+}
+int64_t split_rows(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t max_seqlen_k) {
+  return batch * num_heads * ceil_div(max_seqlen_k, choose_split_tokens(batch, num_kv_heads, max_seqlen_k));
+}
+int64_t persistent_rows(int64_t num_heads, int64_t num_kv_heads) {
+  return 2 * static_cast<int64_t>(device_cu_count()) * kMaxWgsPerCu * (num_heads / num_kv_heads);
 }
 
 }  // namespace
 
 extern "C" int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
                                                        int64_t max_seqlen_k) {
-  return choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
+  return use_persistent(batch, num_kv_heads, max_seqlen_k) ? 0
+                                                           : choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
+}
+
+extern "C" void oxide_set_decode_path(int path) {
+  g_decode_path.store(path == 1 || path == 2 ? path : 0, std::memory_order_relaxed);
 }
 
 extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
@@ -619,7 +954,11 @@ extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t n
                                                         int64_t max_seqlen_k) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0)
     return 0;
-  return static_cast<size_t>(workspace_layout(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k).total);
+  // Enough for either path, so a path override between the size query and the
+  // call cannot overrun it.
+  const int64_t rows = std::max(split_rows(batch, num_heads, num_kv_heads, max_seqlen_k),
+                                persistent_rows(num_heads, num_kv_heads));
+  return static_cast<size_t>(workspace_layout(rows, head_dim).total);
 }
 
 namespace {
@@ -663,9 +1002,12 @@ void decode_attention_impl(void* out, const void* q, const void* new_k, const vo
     return;
   }
   DecodeParams p{};
-  const int64_t st = choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
+  const bool persistent = max_seqlen_k > 0 && use_persistent(batch, num_kv_heads, max_seqlen_k);
+  const int64_t st = max_seqlen_k > 0 ? choose_split_tokens(batch, num_kv_heads, max_seqlen_k) : 1;
   const int64_t max_splits = max_seqlen_k > 0 ? ceil_div(max_seqlen_k, st) : 0;
-  const WorkspaceLayout wl = workspace_layout(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k);
+  const WorkspaceLayout wl = workspace_layout(
+      persistent ? persistent_rows(num_heads, num_kv_heads) : split_rows(batch, num_heads, num_kv_heads, max_seqlen_k),
+      head_dim);
   p.q = q;
   p.k = k_cache;
   p.v = v_cache;
@@ -684,7 +1026,7 @@ void decode_attention_impl(void* out, const void* q, const void* new_k, const vo
   p.num_kv_heads = static_cast<int>(num_kv_heads);
   p.block_size = static_cast<int>(page_block_size);
   p.window_left = window_left < 0 ? -1 : window_left;
-  p.split_tokens = static_cast<int>(st);
+  p.split_tokens = persistent ? 0 : static_cast<int>(st);  // 0 selects the persistent path
   p.max_splits = static_cast<int>(max_splits);
   p.batch = static_cast<int>(batch);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
