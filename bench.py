@@ -454,8 +454,10 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": profiled_traffic(args.config, args.separate),
-                     "kernel": "paged_decode_split + paged_decode_merge (one attention call"
-                               + ("" if args.separate else ", append fused") + ")",
+                     "kernel": ("paged_decode_split + paged_decode_merge"
+                                if ox.split_tokens(cfg.batch, H, st.max_seqlen_k)
+                                else "paged_decode_persistent + paged_decode_merge_persistent")
+                               + " (one attention call" + ("" if args.separate else ", append fused") + ")",
                      "algorithmic_bytes": call_bytes},
         **extra,
     }
