@@ -839,37 +839,41 @@ bool dispatch_group(const DecodeParams& p, int64_t batch, int group, hipStream_t
 }
 
 // Workgroups per CU of the persistent path, at most (bounds the workspace).
-constexpr int kMaxWgsPerCu = 4;
+#ifndef OXIDE_PERSIST_MULT
+#define OXIDE_PERSIST_MULT 1  // rounds of the balanced pass: workgroups = resident slots x this
+#endif
+constexpr int kMaxWgsPerCu = 4 * OXIDE_PERSIST_MULT;
 constexpr int kMaxDevices = 64;
 
 int device_cu_count() {
-  static int cache[kMaxDevices] = {0};
+  static std::atomic<int> cache[kMaxDevices] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  int& n = cache[dev % kMaxDevices];
-  if (n == 0) {
-    int v = 0;
+  std::atomic<int>& n = cache[dev % kMaxDevices];
+  int v = n.load(std::memory_order_relaxed);
+  if (v == 0) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    n = v;
+    n.store(v, std::memory_order_relaxed);
   }
-  return n;
+  return v;
 }
 
 template <class Tag, int D, int G>
 void launch_persistent(DecodeParams p, hipStream_t s) {
   // One workgroup per resident slot: CUs x the kernel's occupancy.
-  static int occ_cache[kMaxDevices] = {0};
+  static std::atomic<int> occ_cache[kMaxDevices] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  int& occ = occ_cache[dev % kMaxDevices];
+  int occ = occ_cache[dev % kMaxDevices].load(std::memory_order_relaxed);
   if (occ == 0) {
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_persistent<Tag, D, G>, kThreads, 0) !=
         hipSuccess)
       n = 2;
-    occ = std::max(1, std::min(n, kMaxWgsPerCu));
+    occ = std::max(1, std::min(n, 4));
+    occ_cache[dev % kMaxDevices].store(occ, std::memory_order_relaxed);
   }
-  p.num_wgs = device_cu_count() * occ;
+  p.num_wgs = device_cu_count() * occ * OXIDE_PERSIST_MULT;
   p.num_wgs -= p.num_wgs % kXcds;  // a whole number of workgroups per XCD
   hipLaunchKernelGGL((paged_decode_persistent<Tag, D, G>), dim3(static_cast<unsigned>(p.num_wgs)),
                      dim3(kThreads), 0, s, p);
