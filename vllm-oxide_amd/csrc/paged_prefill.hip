@@ -52,7 +52,6 @@ constexpr int kPfRows = kPfWaves * 32;  // (token, head) rows per workgroup
 constexpr int kPfKeys = 64;             // keys per K/V tile
 constexpr int kPfXcds = 8;
 
-
 struct PrefillParams {
   const void* q;    // [total_q, Hq, D]
   const void* k;    // paged [NB, BS, Hkv, D] or contiguous [total_k, Hkv, D]
