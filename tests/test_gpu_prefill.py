@@ -160,3 +160,23 @@ def test_prefill_rejects_bad_arguments(device):
     q = torch.zeros((4, 8, 128), dtype=torch.float32, device=device)  # f32: not supported
     with pytest.raises(ox.OxideError):
         ox.prefill_attn(q, q, q, cu, cu, 4, 4, 1.0)
+
+
+@pytest.mark.parametrize("window", [-1, 300])
+def test_prefill_last_rows_equal_decode(device, window):
+    """Cross-kernel invariant: the last query row of every prompt sees exactly the keys a
+    decode step over the same cache sees, so the two kernels agree (within the
+    attention tolerance: different accumulation orders)."""
+    import torch
+    import oxide_paged_kv as ox
+    from helpers import assert_attn_close
+
+    lq, lk = [200, 77, 1, 513], [1200, 77, 40, 513]
+    q, kc, vc, cuq, cuk, table = _case(25, lq, lk, 32, 8, 128, 256, "bf16")
+    pre = to_f32(_gpu(device, q, kc, vc, cuq, cuk, table, 0.09, window, "bf16"))
+    last = np.array([int(cuq[b + 1]) - 1 for b in range(len(lq))])
+    dec = ox.decode_attn(to_torch(q[last], "bf16", device), to_torch(kc, "bf16", device),
+                         to_torch(vc, "bf16", device), torch.from_numpy(cuk.view(np.int32)).to(device),
+                         torch.from_numpy(table).to(device), max(lk), 0.09, None if window < 0 else window)
+    torch.cuda.synchronize()
+    assert_attn_close(pre[last], to_f32(dec))

@@ -149,3 +149,19 @@ def test_rope_cache_builder_matches_oracle(device):
     got = ox.rope_cos_sin_cache(4096, 128, 1_000_000.0).numpy()
     want = oracle.rope_cos_sin_cache(4096, 128, 1_000_000.0)
     assert np.array_equal(got, want)
+
+
+def test_prologue_without_append(device):
+    """slot_mapping None: q (and k) are produced, nothing is written to any cache."""
+    import torch
+    import oxide_paged_kv as ox
+
+    qkv, wq, wk, pos = _case(8, 5, 8, 4, 128, "bf16", True)
+    cs = oracle.rope_cos_sin_cache(8192, 128, 1_000_000.0)
+    q_want, k_want = oracle.qk_norm_rope_and_cache(qkv, 8, 4, 128, wq, wk, 1e-6, cs, pos)
+    t = lambda a: to_torch(a, "bf16", device)  # noqa: E731
+    q, k = ox.qk_norm_rope_and_cache(t(qkv), 8, 4, t(wq), t(wk), 1e-6, torch.from_numpy(cs).to(device),
+                                     torch.from_numpy(pos).to(device), return_k=True)
+    torch.cuda.synchronize()
+    _assert_ulp(to_bits(q), q_want, 0.02)
+    _assert_ulp(to_bits(k), k_want, 0.02)
