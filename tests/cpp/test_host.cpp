@@ -415,6 +415,84 @@ static void test_gpu_decode_step() {
   for (void* p : {dk, dv, dq, dout, ds}) (void)hipFree(p);
 }
 
+// PrefillStep: a 24-token prompt behind a 40-token cached prefix (two sequences'
+// worth of checks in one: the prefix keys come from the cache, the prompt's from
+// the append).  Positions 0 and no q/k norm make the prologue an exact split of
+// the qkv rows, so the output is checked against an in-test fp64 causal softmax.
+static void test_gpu_prefill_step() {
+  const std::size_t Hq = 4, H = 2, D = 64, BS = 16, P = 40, T = 24, L = P + T;
+  PagedKVCache cache(1, 8, BS, H, D, OXIDE_DTYPE_BF16);
+  uint64_t s = 777;
+  auto rnd = [&s]() {
+    s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+    return static_cast<float>(static_cast<int64_t>(s >> 11) % 2000 - 1000) / 1000.f;
+  };
+  // Logical block i of the sequence -> physical block table[i].
+  const std::vector<int32_t> table = {5, 2, 7, 0};
+  auto slot_of = [&](std::size_t j) { return static_cast<int64_t>(table[j / BS]) * BS + j % BS; };
+  std::vector<uint16_t> kall(L * H * D), vall(L * H * D), qkv(T * (Hq + 2 * H) * D), q(T * Hq * D);
+  for (auto& x : kall) x = f2bf(rnd());
+  for (auto& x : vall) x = f2bf(rnd());
+  for (std::size_t t = 0; t < T; ++t) {
+    uint16_t* row = qkv.data() + t * (Hq + 2 * H) * D;
+    for (std::size_t i = 0; i < Hq * D; ++i) q[t * Hq * D + i] = row[i] = f2bf(rnd());
+    std::memcpy(row + Hq * D, kall.data() + (P + t) * H * D, H * D * 2);
+    std::memcpy(row + (Hq + H) * D, vall.data() + (P + t) * H * D, H * D * 2);
+  }
+  // The prefix is already in the cache.
+  std::vector<int64_t> pslots;
+  for (std::size_t j = 0; j < P; ++j) pslots.push_back(slot_of(j));
+  void *dk, *dv, *ds, *dqkv, *dq, *dout, *dcs;
+  (void)hipMalloc(&dk, P * H * D * 2);
+  (void)hipMalloc(&dv, P * H * D * 2);
+  (void)hipMalloc(&ds, P * 8);
+  (void)hipMemcpy(dk, kall.data(), P * H * D * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(dv, vall.data(), P * H * D * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(ds, pslots.data(), P * 8, hipMemcpyHostToDevice);
+  cache.reshape_and_cache(0, dk, dv, static_cast<const int64_t*>(ds), P, nullptr);
+  (void)hipMalloc(&dqkv, qkv.size() * 2);
+  (void)hipMalloc(&dq, T * Hq * D * 2);
+  (void)hipMalloc(&dout, T * Hq * D * 2);
+  (void)hipMemcpy(dqkv, qkv.data(), qkv.size() * 2, hipMemcpyHostToDevice);
+  const std::vector<float> cs = rope_cos_sin_cache(8, D, 1e6f);
+  (void)hipMalloc(&dcs, cs.size() * 4);
+  (void)hipMemcpy(dcs, cs.data(), cs.size() * 4, hipMemcpyHostToDevice);
+  std::vector<int64_t> slots;
+  for (std::size_t t = 0; t < T; ++t) slots.push_back(slot_of(P + t));
+  PrefillStep step(cache, Hq);
+  step.upload(build_prefill_metadata({static_cast<uint32_t>(T)}, {static_cast<uint32_t>(L)}, slots), {table},
+              std::vector<int32_t>(T, 0), nullptr);
+  const float scale = 1.f / std::sqrt(static_cast<float>(D));
+  step.run_layer(0, dqkv, nullptr, nullptr, 1e-6, static_cast<const float*>(dcs), 8, dq, dout, scale, -1, nullptr);
+  std::vector<uint16_t> out(T * Hq * D);
+  (void)hipMemcpy(out.data(), dout, out.size() * 2, hipMemcpyDeviceToHost);
+  double max_err = 0;
+  for (std::size_t t = 0; t < T; ++t)
+    for (std::size_t h = 0; h < Hq; ++h) {
+      const std::size_t kh = h / (Hq / H), nk = P + t + 1;  // causal, aligned bottom-right
+      std::vector<double> sc(nk);
+      double mx = -1e300, l = 0;
+      for (std::size_t j = 0; j < nk; ++j) {
+        double dot = 0;
+        for (std::size_t d = 0; d < D; ++d)
+          dot += static_cast<double>(bf2f(q[(t * Hq + h) * D + d])) * bf2f(kall[(j * H + kh) * D + d]);
+        mx = std::max(mx, sc[j] = dot * scale);
+      }
+      for (auto& x : sc) l += (x = std::exp(x - mx));
+      for (std::size_t d = 0; d < D; ++d) {
+        double o = 0;
+        for (std::size_t j = 0; j < nk; ++j) o += sc[j] / l * bf2f(vall[(j * H + kh) * D + d]);
+        max_err = std::max(max_err, std::fabs(bf2f(out[(t * Hq + h) * D + d]) - o));
+      }
+    }
+  CHECK(max_err <= 2e-2);
+  // The prompt's K/V landed in their slots.
+  std::vector<uint16_t> kc(8 * BS * H * D);
+  (void)hipMemcpy(kc.data(), cache.k_cache(0), kc.size() * 2, hipMemcpyDeviceToHost);
+  CHECK(std::memcmp(kc.data() + slot_of(L - 1) * H * D, kall.data() + (L - 1) * H * D, H * D * 2) == 0);
+  for (void* ptr : {dk, dv, ds, dqkv, dq, dout, dcs}) (void)hipFree(ptr);
+}
+
 int main(int argc, char** argv) {
   const std::string mode = argc > 1 ? argv[1] : "cpu";
   if (mode == "hash" && argc == 4) {
@@ -435,6 +513,7 @@ int main(int argc, char** argv) {
   } else if (mode == "gpu") {
     test_gpu_append_known_answer();
     test_gpu_cow_all_layers();
+    test_gpu_prefill_step();
     test_gpu_decode_step();
   } else {
     std::printf("usage: test_host cpu|gpu|hash <seed> <hex>\n");

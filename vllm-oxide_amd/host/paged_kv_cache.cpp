@@ -164,4 +164,78 @@ void DecodeStep::run_layer(std::size_t layer, const void* q, const void* key, co
   check_lib("paged_decode_attention_append");
 }
 
+PrefillStep::PrefillStep(const PagedKVCache& cache, std::size_t num_heads)
+    : cache_(cache), num_heads_(num_heads) {}
+
+PrefillStep::~PrefillStep() {
+  if (d_buf_) (void)hipFree(d_buf_);
+}
+
+void PrefillStep::upload(const AttnMetadata& meta, const std::vector<std::vector<int32_t>>& block_table,
+                         const std::vector<int32_t>& positions, hipStream_t stream) {
+  if (!meta.is_prefill) throw std::invalid_argument("PrefillStep needs prefill metadata");
+  batch_ = meta.cu_seqlens_q.empty() ? 0 : meta.cu_seqlens_q.size() - 1;
+  num_tokens_ = batch_ ? meta.cu_seqlens_q.back() : 0;
+  if (batch_ == 0) return;
+  if (block_table.size() != batch_ || positions.size() != num_tokens_ || meta.slot_mapping.size() != num_tokens_)
+    throw std::invalid_argument("PrefillStep: block_table / positions / slot_mapping do not match the batch");
+  const PaddedTable t = pad_block_table(block_table);
+  max_blocks_ = t.width;
+  max_seqlen_q_ = meta.max_seqlen_q;
+  max_seqlen_k_ = meta.max_seqlen_k;
+  // The previous step's asynchronous upload may still read the staging copies.
+  check(hipStreamSynchronize(stream), "hipStreamSynchronize");
+  h_cuq_ = meta.cu_seqlens_q;
+  h_cuk_ = meta.cu_seqlens_k;
+  h_table_ = t.data;
+  h_pos_ = positions;
+  h_slots_ = meta.slot_mapping;
+  auto part = [](std::size_t bytes) { return round_up(std::max<std::size_t>(bytes, 1), 256); };
+  off_cuk_ = part(h_cuq_.size() * 4);
+  off_table_ = off_cuk_ + part(h_cuk_.size() * 4);
+  off_pos_ = off_table_ + part(h_table_.size() * 4);
+  off_slots_ = off_pos_ + part(h_pos_.size() * 4);
+  const std::size_t total = off_slots_ + part(h_slots_.size() * 8);
+  if (total > cap_) {
+    if (d_buf_) check(hipFree(d_buf_), "hipFree");
+    d_buf_ = nullptr;
+    check(hipMalloc(&d_buf_, total), "hipMalloc(PrefillStep)");
+    cap_ = total;
+  }
+  char* d = static_cast<char*>(d_buf_);
+  check(hipMemcpyAsync(d, h_cuq_.data(), h_cuq_.size() * 4, hipMemcpyHostToDevice, stream), "upload cu_seqlens_q");
+  check(hipMemcpyAsync(d + off_cuk_, h_cuk_.data(), h_cuk_.size() * 4, hipMemcpyHostToDevice, stream),
+        "upload cu_seqlens_k");
+  check(hipMemcpyAsync(d + off_table_, h_table_.data(), h_table_.size() * 4, hipMemcpyHostToDevice, stream),
+        "upload block_table");
+  check(hipMemcpyAsync(d + off_pos_, h_pos_.data(), h_pos_.size() * 4, hipMemcpyHostToDevice, stream),
+        "upload positions");
+  check(hipMemcpyAsync(d + off_slots_, h_slots_.data(), h_slots_.size() * 8, hipMemcpyHostToDevice, stream),
+        "upload slot_mapping");
+}
+
+void PrefillStep::run_layer(std::size_t layer, const void* qkv, const void* q_norm_weight,
+                            const void* k_norm_weight, double eps, const float* cos_sin,
+                            std::size_t max_position, void* q_scratch, void* out, float softmax_scale,
+                            int32_t window_left, hipStream_t stream) {
+  if (batch_ == 0 || num_tokens_ == 0) return;
+  const char* d = static_cast<const char*>(d_buf_);
+  const int64_t Hq = static_cast<int64_t>(num_heads_), Hkv = static_cast<int64_t>(cache_.num_kv_heads()),
+                D = static_cast<int64_t>(cache_.head_dim());
+  ::qk_norm_rope_and_cache(q_scratch, nullptr, qkv, (Hq + 2 * Hkv) * D, q_norm_weight, k_norm_weight, eps,
+                           cos_sin, static_cast<int64_t>(max_position),
+                           reinterpret_cast<const int32_t*>(d + off_pos_), cache_.k_cache(layer),
+                           cache_.v_cache(layer), reinterpret_cast<const int64_t*>(d + off_slots_),
+                           static_cast<int64_t>(num_tokens_), Hq, Hkv, D, cache_.dtype(), stream);
+  check_lib("qk_norm_rope_and_cache");
+  ::paged_prefill_attention(out, q_scratch, cache_.k_cache(layer), cache_.v_cache(layer),
+                            reinterpret_cast<const uint32_t*>(d), reinterpret_cast<const uint32_t*>(d + off_cuk_),
+                            reinterpret_cast<const int32_t*>(d + off_table_), static_cast<int64_t>(max_blocks_),
+                            static_cast<int64_t>(cache_.num_blocks()), static_cast<int64_t>(batch_), Hq, Hkv, D,
+                            static_cast<int64_t>(cache_.block_size()), static_cast<int64_t>(max_seqlen_q_),
+                            static_cast<int64_t>(max_seqlen_k_), window_left, softmax_scale, cache_.dtype(),
+                            stream);
+  check_lib("paged_prefill_attention");
+}
+
 }  // namespace oxide::host

@@ -97,4 +97,45 @@ class DecodeStep {
   std::size_t cap_cu_ = 0, cap_table_ = 0, cap_slots_ = 0, cap_ws_ = 0;
 };
 
+// The prefill step on the paged cache: per step, upload cu_seqlens_q / _k, the
+// padded block table, the slot mapping and the positions once; per layer, run
+// the attention prologue (q/k norm + RoPE + append of the prompt's K/V,
+// qwen3.rs:161-199) and paged prefill attention over every key of the
+// sequence, cached prefix included.  The reference's prefill reads only the
+// projection K/V (flash_attn_varlen, engine/mod.rs:172,195) and so cannot use
+// a prefix hit; here the prefix keys are simply the first Lk - Lq keys.
+class PrefillStep {
+ public:
+  PrefillStep(const PagedKVCache& cache, std::size_t num_heads);
+  ~PrefillStep();
+  PrefillStep(const PrefillStep&) = delete;
+  PrefillStep& operator=(const PrefillStep&) = delete;
+
+  // meta from build_prefill_metadata (its block_table is not used);
+  // block_table: each sequence's block ids (covering its kv length);
+  // positions: the position of each scheduled token (engine/mod.rs:176-183).
+  void upload(const AttnMetadata& meta, const std::vector<std::vector<int32_t>>& block_table,
+              const std::vector<int32_t>& positions, hipStream_t stream);
+
+  // Layer `layer`: qkv [T, (Hq + 2 Hkv) D] -> q_scratch [T, Hq, D] (normed,
+  // rotated), K/V appended at the slot mapping, out [T, Hq, D].  Norm weights
+  // may be null (no q/k norm); cos_sin is the fp32 [max_position, D] table.
+  void run_layer(std::size_t layer, const void* qkv, const void* q_norm_weight, const void* k_norm_weight,
+                 double eps, const float* cos_sin, std::size_t max_position, void* q_scratch, void* out,
+                 float softmax_scale, int32_t window_left, hipStream_t stream);
+
+  std::size_t num_tokens() const { return num_tokens_; }
+
+ private:
+  const PagedKVCache& cache_;
+  std::size_t num_heads_;
+  std::size_t batch_ = 0, num_tokens_ = 0, max_blocks_ = 0, max_seqlen_q_ = 0, max_seqlen_k_ = 0;
+  std::vector<uint32_t> h_cuq_, h_cuk_;
+  std::vector<int32_t> h_table_, h_pos_;
+  std::vector<int64_t> h_slots_;
+  void* d_buf_ = nullptr;  // cu_q | cu_k | table | positions | slots, 256-byte aligned parts
+  std::size_t cap_ = 0;
+  std::size_t off_cuk_ = 0, off_table_ = 0, off_pos_ = 0, off_slots_ = 0;
+};
+
 }  // namespace oxide::host
