@@ -270,6 +270,74 @@ static void test_cow() {
   CHECK(pool.num_free_blocks() == 8);
 }
 
+// Randomised sequences of allocate / fork / append (with CoW) / deallocate:
+// after every operation each block's ref_count equals the number of live block
+// tables holding it, used blocks are exactly those with references, and the
+// free list holds the rest; at the end everything is free again.
+static void test_pool_random_ops() {
+  const std::size_t NB = 24;
+  BlockPool pool(NB, kBlockSize);  // Sequence counts blocks of kBlockSize (sequence.rs:20)
+  std::vector<Sequence> live;
+  std::size_t copies = 0, new_blocks = 0;
+  uint64_t s = 99;
+  auto rnd = [&s](uint64_t n) {
+    s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+    return static_cast<std::size_t>((s >> 33) % n);
+  };
+  auto check_invariants = [&]() {
+    std::vector<std::size_t> refs(NB, 0);
+    for (const auto& q : live)
+      for (std::size_t id : q.block_table) ++refs[id];
+    std::size_t used = 0;
+    for (std::size_t id = 0; id < NB; ++id) {
+      CHECK(pool.block(id).ref_count == refs[id]);
+      CHECK(pool.is_used(id) == (refs[id] > 0));
+      used += refs[id] > 0;
+    }
+    CHECK(pool.num_free_blocks() + used == NB);
+  };
+  for (int step = 0; step < 20000; ++step) {
+    const std::size_t op = rnd(10);
+    if (op < 3) {  // new sequence
+      // Half of them end at or next to a block boundary, so appends cross it.
+      const std::size_t n = rnd(2) ? 1 + rnd(700) : kBlockSize * (1 + rnd(2)) - rnd(2);
+      Sequence q(iota(0, static_cast<uint32_t>(n)));
+      const auto cached = pool.can_allocate(q);
+      if (cached) {
+        pool.allocate(q, *cached);
+        live.push_back(q);
+      }
+    } else if (op < 5 && !live.empty()) {  // fork
+      Sequence child;
+      pool.fork(live[rnd(live.size())], child);
+      live.push_back(child);
+    } else if (op < 8 && !live.empty()) {  // append tokens, one at a time
+      Sequence& q = live[rnd(live.size())];
+      q.append_token(static_cast<uint32_t>(rnd(1000)));
+      if (pool.can_append_cow(q)) {
+        const std::size_t before = q.block_table.size();
+        if (pool.may_append_cow(q)) ++copies;
+        if (q.block_table.size() > before) ++new_blocks;
+        CHECK(q.block_table.size() == q.num_blocks());
+      } else {
+        q.token_ids.pop_back();  // no room: undo (the scheduler would preempt)
+        --q.num_tokens;
+      }
+    } else if (!live.empty()) {  // finish a sequence
+      const std::size_t i = rnd(live.size());
+      pool.deallocate(live[i]);
+      live.erase(live.begin() + static_cast<std::ptrdiff_t>(i));
+    }
+    check_invariants();
+  }
+  for (auto& q : live) pool.deallocate(q);
+  live.clear();
+  check_invariants();
+  CHECK(pool.num_free_blocks() == NB);
+  std::printf("random ops: %zu copies, %zu new blocks\n", copies, new_blocks);
+  CHECK(copies > 20 && new_blocks > 10);  // both append paths were exercised
+}
+
 static uint16_t f2bf(float f) {
   uint32_t u;
   std::memcpy(&u, &f, 4);
@@ -510,6 +578,7 @@ int main(int argc, char** argv) {
     test_slot_mapping();
     test_block_pool();
     test_cow();
+    test_pool_random_ops();
   } else if (mode == "gpu") {
     test_gpu_append_known_answer();
     test_gpu_cow_all_layers();
