@@ -119,7 +119,8 @@ void gather_blocks(void* key_dst, void* value_dst, const void* key_cache, const 
  *
  * Query head h reads kv head h / (num_heads / num_kv_heads).  A sequence with
  * L_b == 0 produces zeros.  Supported: dtype f16 or bf16, head_dim 64 or 128,
- * num_heads / num_kv_heads in {1, 2, 4, 8, 16}, page_block_size a positive
+ * num_heads / num_kv_heads in 1..8 or 16 (Qwen3-14B has 5, Qwen2.5-7B 7),
+ * page_block_size a positive
  * multiple of 16.  workspace must hold
  * paged_decode_attention_workspace_size(...) bytes for the same arguments (no
  * initialisation needed).  Calls that share a workspace must not overlap in

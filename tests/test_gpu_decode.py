@@ -61,6 +61,10 @@ CASES = [
     (3, 16, 8, 128, 256, 30, [2000, 700, 101], 100, "bf16"),            # window 100
     (2, 16, 8, 128, 256, 10, [600, 5], 0, "bf16"),                      # window 0: last key only
     (5, 16, 8, 128, 256, 20, [0, 10, 0, 1, 300], -1, "bf16"),           # empty sequences
+    (3, 40, 8, 128, 256, 40, [3000, 257, 1200], -1, "bf16"),            # G=5 (Qwen3-14B heads)
+    (2, 28, 4, 128, 16, 300, [2100, 77], 500, "bf16"),                  # G=7 (Qwen2.5-7B), window
+    (2, 12, 4, 64, 256, 20, [900, 31], -1, "f16"),                      # G=3, D=64
+    (2, 24, 4, 128, 256, 20, [1500, 256], -1, "bf16"),                  # G=6
 ]
 
 

@@ -831,7 +831,11 @@ bool dispatch_group(const DecodeParams& p, int64_t batch, int group, hipStream_t
   switch (group) {
     case 1: launch_split<Tag, D, 1>(p, batch, s); return true;
     case 2: launch_split<Tag, D, 2>(p, batch, s); return true;
+    case 3: launch_split<Tag, D, 3>(p, batch, s); return true;
     case 4: launch_split<Tag, D, 4>(p, batch, s); return true;
+    case 5: launch_split<Tag, D, 5>(p, batch, s); return true;
+    case 6: launch_split<Tag, D, 6>(p, batch, s); return true;
+    case 7: launch_split<Tag, D, 7>(p, batch, s); return true;
     case 8: launch_split<Tag, D, 8>(p, batch, s); return true;
     case 16: launch_split<Tag, D, 16>(p, batch, s); return true;
     default: return false;
@@ -887,7 +891,11 @@ bool dispatch_persistent(const DecodeParams& p, int group, hipStream_t s) {
   switch (group) {
     case 1: launch_persistent<Tag, D, 1>(p, s); return true;
     case 2: launch_persistent<Tag, D, 2>(p, s); return true;
+    case 3: launch_persistent<Tag, D, 3>(p, s); return true;
     case 4: launch_persistent<Tag, D, 4>(p, s); return true;
+    case 5: launch_persistent<Tag, D, 5>(p, s); return true;
+    case 6: launch_persistent<Tag, D, 6>(p, s); return true;
+    case 7: launch_persistent<Tag, D, 7>(p, s); return true;
     case 8: launch_persistent<Tag, D, 8>(p, s); return true;
     case 16: launch_persistent<Tag, D, 16>(p, s); return true;
     default: return false;
@@ -995,7 +1003,7 @@ void decode_attention_impl(void* out, const void* q, const void* new_k, const vo
   }
   const int64_t group = num_heads / num_kv_heads;
   if ((head_dim != 64 && head_dim != 128) || page_block_size % 16 != 0 ||
-      (group != 1 && group != 2 && group != 4 && group != 8 && group != 16)) {
+      group < 1 || (group > 8 && group != 16)) {
     oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
     return;
   }
