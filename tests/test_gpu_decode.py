@@ -408,3 +408,33 @@ def test_decode_fused_append_full_size(device, cfg_id):
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     assert torch.equal(k2.view(torch.int16), kc.view(torch.int16))
     assert torch.equal(v2.view(torch.int16), vc.view(torch.int16))
+
+
+def test_kernels_vs_committed_goldens(device):
+    """Decode and prefill kernels against the committed fp64 goldens (small seeded
+    cases, G 1/2/4/8, window none/100), within the attention tolerance."""
+    import importlib.util
+    from pathlib import Path
+
+    import torch
+    import oxide_paged_kv as ox
+
+    here = Path(__file__).parent / "golden"
+    gold = np.load(here / "attention_goldens.npz")
+    spec = importlib.util.spec_from_file_location("gold", here / "make_attention_goldens.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    for i, sp in enumerate(mod.SPECS):
+        q, kc, vc, cuq, cuk, table, scale = mod.case_inputs(sp)
+        print(f"golden case{i} {sp[0]} G={sp[2]} window={sp[7]}", flush=True)
+        t = lambda a: to_torch(a, "bf16", device)  # noqa: E731
+        w = None if sp[7] < 0 else sp[7]
+        if sp[0] == "decode":
+            out = ox.decode_attn(t(q), t(kc), t(vc), torch.from_numpy(cuk.view(np.int32)).to(device),
+                                 torch.from_numpy(table).to(device), int(np.diff(cuk).max()), scale, w, sp[4])
+        else:
+            out = ox.prefill_attn(t(q), t(kc), t(vc), torch.from_numpy(cuq.view(np.int32)).to(device),
+                                  torch.from_numpy(cuk.view(np.int32)).to(device), int(np.diff(cuq).max()),
+                                  int(np.diff(cuk).max()), scale, torch.from_numpy(table).to(device), w)
+        torch.cuda.synchronize()
+        assert_attn_close(to_f32(out), gold[f"case{i}"])

@@ -423,3 +423,24 @@ def test_prologue_closed_forms():
     la = np.hypot(a[..., :D // 2], a[..., D // 2:])
     lb = np.hypot(b[..., :D // 2], b[..., D // 2:])
     np.testing.assert_allclose(lb, la, rtol=2e-2, atol=1e-2)
+
+
+# --------------------------------------------------- committed attention goldens
+def test_attention_goldens_reproduce():
+    """The committed fixture (tests/golden/attention_goldens.npz, written by
+    tests/golden/make_attention_goldens.py from seeded inputs) still equals what the
+    fp64 oracle computes: a regression pin of the oracle and of the input generator."""
+    import importlib.util
+
+    gold = np.load(Path(__file__).parent / "golden" / "attention_goldens.npz")
+    spec = importlib.util.spec_from_file_location("gold", Path(__file__).parent / "golden" / "make_attention_goldens.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    assert len(gold.files) == len(mod.SPECS)
+    for i, sp in enumerate(mod.SPECS):
+        q, kc, vc, cuq, cuk, table, scale = mod.case_inputs(sp)
+        if sp[0] == "decode":
+            o = oracle.paged_decode_attention(q, kc, vc, cuk, table, scale, sp[7], "bf16", use_f64=True)
+        else:
+            o = oracle.prefill_attention(q, kc, vc, cuq, cuk, scale, table, sp[7], "bf16", use_f64=True)
+        np.testing.assert_array_equal(o.astype(np.float32), gold[f"case{i}"], err_msg=f"case{i}")
