@@ -412,6 +412,8 @@ static void test_gpu_cow_all_layers() {
     }
   CHECK(got == want);
   CHECK(throws([&] { cache.copy_blocks_all_layers({{1, 4}}, nullptr); }));
+  CHECK(throws([&] { cache.copy_blocks_all_layers({{1, 2}, {2, 3}}, nullptr); }));  // dst 2 is a src
+  CHECK(throws([&] { cache.copy_blocks_all_layers({{1, 2}, {3, 2}}, nullptr); }));  // dst 2 twice
 }
 
 static void test_gpu_decode_step() {

@@ -2,6 +2,7 @@
 #include "paged_kv_cache.hpp"
 
 #include <algorithm>
+#include <unordered_set>
 
 namespace oxide::host {
 
@@ -78,8 +79,17 @@ void PagedKVCache::copy_blocks(std::size_t layer, const int64_t* block_mapping,
 void PagedKVCache::copy_blocks_all_layers(const std::vector<std::pair<std::size_t, std::size_t>>& pairs,
                                           hipStream_t stream) {
   if (pairs.empty()) return;
-  for (const auto& pr : pairs)
+  // The copy kernel runs every pair at once: a destination that is also a
+  // source, or written twice, would race (copy_blocks.cu:20-27 leaves this
+  // unchecked).  The pairs are on the host here, so check them.
+  std::unordered_set<std::size_t> srcs, dsts;
+  for (const auto& pr : pairs) {
     if (pr.first >= num_blocks_ || pr.second >= num_blocks_) throw std::out_of_range("block id");
+    srcs.insert(pr.first);
+    if (!dsts.insert(pr.second).second) throw std::invalid_argument("copy_blocks: a block is written twice");
+  }
+  for (std::size_t d : dsts)
+    if (srcs.count(d)) throw std::invalid_argument("copy_blocks: a destination block is also a source");
   // The previous call's upload may still read the staging copy.
   check(hipStreamSynchronize(stream), "hipStreamSynchronize");
   h_map_.clear();
