@@ -42,14 +42,21 @@ TRAFFIC_PROFILE = {(3, False): REPO / "profiles" / "paged_decode_cfg3.md",
                    (5, False): REPO / "profiles" / "paged_decode_cfg5.md"}
 
 
-def profiled_traffic(config: int, separate: bool):
-    path = TRAFFIC_PROFILE.get((config, separate))
+def _profile_value(path, key: str):
     if path is None or not path.exists():
         return None
     for line in path.read_text().splitlines():
-        if line.startswith("traffic_bytes_per_attention_call:"):
+        if line.startswith(key + ":"):
             return int(line.split(":")[1])
     return None
+
+
+def profiled_traffic(config: int, separate: bool):
+    return _profile_value(TRAFFIC_PROFILE.get((config, separate)), "traffic_bytes_per_attention_call")
+
+
+# PMC traffic of the prologue at its default size (16,384 tokens, Qwen3-8B heads).
+PROLOGUE_PROFILE = REPO / "profiles" / "qk_norm_rope_cache_16k.md"
 
 
 def cpu_baseline(cfg, seed: int, threads: int, min_seconds: float = 10.0) -> dict:
@@ -260,8 +267,12 @@ def prologue_main(args) -> int:
     vc = torch.zeros_like(kc)
     slots = torch.randperm(nb * BS, generator=g, device=dev)[:T].contiguous()
 
+    q_out = torch.empty((T, Hq, D), dtype=torch.bfloat16, device=dev)
+    layer_qkv = [qkv[i] for i in range(layers)]
+
     def call(i):
-        ox.qk_norm_rope_and_cache(qkv[i % layers], Hq, Hkv, w[0], w[1], 1e-6, cs, pos, kc, vc, slots)
+        ox.qk_norm_rope_and_cache(layer_qkv[i % layers], Hq, Hkv, w[0], w[1], 1e-6, cs, pos, kc, vc, slots,
+                                  q_out=q_out)
 
     for i in range(args.warmup):
         call(i)
@@ -286,7 +297,8 @@ def prologue_main(args) -> int:
                    "head_dim": D},
         "call_us": round(us, 2),
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": _profile_value(PROLOGUE_PROFILE, "traffic_bytes_per_call") if T == 16384 else None,
                      "kernel": "qk_norm_rope_cache_kernel", "algorithmic_bytes": nbytes},
     }
     if not args.no_cpu_baseline:
@@ -298,8 +310,8 @@ def prologue_main(args) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 50; --prologue 500)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 10; --prologue 50)")
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--layers", type=int, default=0, help="distinct layers to rotate over (0 = auto)")
     ap.add_argument("--seed", type=int, default=0)
@@ -315,6 +327,11 @@ def main() -> int:
                     help="time the fused q/k norm + RoPE + KV append instead of the decode step")
     ap.add_argument("--tokens", type=int, default=16384, help="--prologue: tokens per call")
     args = ap.parse_args()
+    # A prologue call is ~0.1 ms: more of them keep the timed region near 50 ms.
+    if args.steps is None:
+        args.steps = 500 if args.prologue else 50
+    if args.warmup is None:
+        args.warmup = 50 if args.prologue else 10
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)

@@ -10,6 +10,10 @@
 #include <string>
 #include <vector>
 
+#include <atomic>
+#include <thread>
+
+#include "exact_div.hpp"
 #include "oxide_host.hpp"
 #include "paged_kv_cache.hpp"
 
@@ -563,6 +567,63 @@ static void test_gpu_prefill_step() {
   for (void* ptr : {dk, dv, ds, dqkv, dq, dout, dcs}) (void)hipFree(ptr);
 }
 
+// The fast divide of the attention prologue (exact_div.hpp) against the
+// correctly rounded x / b.  The quotient's significand depends only on the
+// significands of x and b while every step stays normal, so checking every
+// f16 significand of x (a superset of bf16's) against every fp32 significand
+// of b ("div full", 8.6e9 pairs) covers the whole domain; the default run
+// takes every 97th b significand.  Edge exponents and signed zeros on top.
+static float u2f(uint32_t u) {
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+static void test_exact_div(bool full) {
+  const uint32_t step = full ? 1 : 97;
+  std::atomic<long long> bad{0}, checked{0};
+  const unsigned nth = std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
+  std::vector<std::thread> pool;
+  for (unsigned t = 0; t < nth; ++t)
+    pool.emplace_back([&, t] {
+      long long b_bad = 0, n = 0;
+      for (uint32_t mb = t * step; mb < (1u << 23); mb += nth * step) {
+        const float b = u2f((127u << 23) | mb);
+        const float y = 1.0f / b;
+        for (uint32_t ma = 0; ma < 1024; ++ma) {
+          const float x = u2f((127u << 23) | (ma << 13));
+          b_bad += oxide::exact_div(x, b, y) != x / b;
+          ++n;
+        }
+      }
+      bad += b_bad;
+      checked += n;
+    });
+  for (auto& th : pool) th.join();
+  CHECK(bad.load() == 0);
+  CHECK(checked.load() > 0);
+  // Domain edges: exponents of x and b at their limits, both signs, zeros.
+  uint64_t rng = 88172645463325252ull;
+  for (int i = 0; i < 200000; ++i) {
+    rng ^= rng << 13; rng ^= rng >> 7; rng ^= rng << 17;
+    const float b = u2f(((127u - 32 + static_cast<uint32_t>(rng % 65)) << 23) | ((rng >> 8) & 0x7fffffu));
+    const uint32_t ex = 127u - 60 + static_cast<uint32_t>((rng >> 40) % 125);  // 2^-60 .. 2^64
+    float x = u2f((ex << 23) | ((static_cast<uint32_t>(rng >> 32) & 0x3ffu) << 13));
+    if (rng & (1ull << 63)) x = -x;
+    if (!oxide::exact_div_divisor_ok(b) || !oxide::exact_div_dividend_ok(x)) continue;
+    const float y = 1.0f / b;
+    CHECK(oxide::exact_div(x, b, y) == x / b);
+  }
+  for (float b : {0x1p-32f, 1.0f, 3.0f, 0x1p32f}) {
+    const float y = 1.0f / b;
+    CHECK(std::signbit(oxide::exact_div(-0.0f, b, y)) && oxide::exact_div(-0.0f, b, y) == 0.0f);
+    CHECK(!std::signbit(oxide::exact_div(0.0f, b, y)) && oxide::exact_div(0.0f, b, y) == 0.0f);
+  }
+  CHECK(!oxide::exact_div_divisor_ok(0x1p-33f) && !oxide::exact_div_divisor_ok(INFINITY) &&
+        !oxide::exact_div_divisor_ok(NAN));
+  CHECK(!oxide::exact_div_dividend_ok(0x1p-61f) && !oxide::exact_div_dividend_ok(NAN));
+  std::printf("exact_div: %lld pairs checked\n", static_cast<long long>(checked.load()));
+}
+
 int main(int argc, char** argv) {
   const std::string mode = argc > 1 ? argv[1] : "cpu";
   if (mode == "hash" && argc == 4) {
@@ -581,13 +642,16 @@ int main(int argc, char** argv) {
     test_block_pool();
     test_cow();
     test_pool_random_ops();
+    test_exact_div(false);
+  } else if (mode == "div") {
+    test_exact_div(argc > 2 && std::string(argv[2]) == "full");
   } else if (mode == "gpu") {
     test_gpu_append_known_answer();
     test_gpu_cow_all_layers();
     test_gpu_prefill_step();
     test_gpu_decode_step();
   } else {
-    std::printf("usage: test_host cpu|gpu|hash <seed> <hex>\n");
+    std::printf("usage: test_host cpu|gpu|div [full]|hash <seed> <hex>\n");
     return 2;
   }
   std::printf("%s: %d failures\n", mode.c_str(), g_failures);

@@ -54,7 +54,7 @@ def test_error_paths_without_launch():
     L.paged_decode_attention(*ptrs, 1, 4, 1, 32, 8, 96, 256, 10, -1, 0.1, dummy, 1 << 30, 1, None)
     assert L.oxide_last_error() == 3
     L.oxide_clear_error()
-    L.paged_decode_attention(*ptrs, 1, 4, 1, 24, 8, 128, 256, 10, -1, 0.1, dummy, 1 << 30, 1, None)
+    L.paged_decode_attention(*ptrs, 1, 4, 1, 72, 8, 128, 256, 10, -1, 0.1, dummy, 1 << 30, 1, None)  # group 9
     assert L.oxide_last_error() == 3
     L.oxide_clear_error()
     L.paged_decode_attention(*ptrs, 1, 4, 1, 32, 8, 128, 256, 10, -1, 0.1, dummy, 1 << 30, 2, None)

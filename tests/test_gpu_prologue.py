@@ -165,3 +165,96 @@ def test_prologue_without_append(device):
     torch.cuda.synchronize()
     _assert_ulp(to_bits(q), q_want, 0.02)
     _assert_ulp(to_bits(k), k_want, 0.02)
+
+
+def _exact_sum_case(seed, T, Hq, Hkv, D, dtype, tiny_heads=()):
+    """qkv rows whose sums of squares are exact in any order: elements k / 8 with
+    |k| <= 16 (squares are multiples of 2^-6, a head's sum stays below 2^11), so
+    GPU and oracle see the same mean and the whole chain must agree bit for bit.
+    Heads listed in tiny_heads hold k * 2^-70 instead: below the fast divide's
+    domain, so they take the general divide (eps dominates their mean)."""
+    rng = np.random.default_rng(seed)
+    H = Hq + 2 * Hkv
+    x = (rng.integers(-16, 17, (T, H, D)) / 8.0).astype(np.float32)
+    for h in tiny_heads:
+        x[:, h, :] = rng.integers(-16, 17, (T, D)).astype(np.float32) * np.float32(2.0 ** -70)
+    x[0, 0, :3] = 0.0
+    x[0, 0, 3] = -0.0
+    qkv = oracle.float_to_half(x.reshape(T, H * D), dtype)
+    w = oracle.float_to_half(1.0 + rng.integers(-8, 9, (2, D)) / 64.0, dtype)
+    pos = rng.integers(0, 8192, T).astype(np.int32)
+    return qkv, w[0], w[1], pos
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("D", [128, 64])
+def test_prologue_bit_exact_when_sums_are_exact(device, dtype, D):
+    """Pins the per-element arithmetic (the divide by the rms, both roundings, the
+    weight, the rotation) bit for bit: the only freedom, the order of the sum of
+    squares, is removed by inputs whose sums are exact.  Heads 1 (a q head) and
+    Hq + 1 (a k head) take the general-divide path."""
+    import torch
+    import oxide_paged_kv as ox
+
+    T, Hq, Hkv = 33, 16, 4
+    print(f"prologue exact-sum D={D} {dtype}", flush=True)
+    tiny = (1, Hq + 1) if dtype == "bf16" else ()
+    qkv, wq, wk, pos = _exact_sum_case(11, T, Hq, Hkv, D, dtype, tiny_heads=tiny)
+    cs = oracle.rope_cos_sin_cache(8192, D, 1_000_000.0)
+    q_want, k_want = oracle.qk_norm_rope_and_cache(qkv, Hq, Hkv, D, wq, wk, 1e-6, cs, pos, dtype=dtype)
+    t = lambda a: to_torch(a, dtype, device)  # noqa: E731
+    q, k = ox.qk_norm_rope_and_cache(t(qkv), Hq, Hkv, t(wq), t(wk), 1e-6, torch.from_numpy(cs).to(device),
+                                     torch.from_numpy(pos).to(device), return_k=True)
+    torch.cuda.synchronize()
+    got_q, got_k = to_bits(q), to_bits(k)
+    assert np.array_equal(got_q, q_want), f"{int((got_q != q_want).sum())} q elements differ"
+    assert np.array_equal(got_k, k_want), f"{int((got_k != k_want).sum())} k elements differ"
+    if tiny:
+        assert got_q.reshape(T, Hq, D)[:, 1].any()  # the tiny heads did not flush to zero
+
+
+def test_prologue_nan_propagates(device):
+    """A NaN input element makes NaN outputs where the oracle has them (payload bits
+    after fp32 arithmetic are the hardware's own, so NaN-ness is compared), and the
+    rest of the head and of the batch is unaffected."""
+    import torch
+    import oxide_paged_kv as ox
+
+    T, Hq, Hkv, D = 4, 8, 2, 128
+    qkv, wq, wk, pos = _case(12, T, Hq, Hkv, D, "bf16", True)
+    qkv[1, 5 * D + 7] = 0x7FC1           # q head 5 of token 1 (normed: the whole head turns NaN)
+    qkv[2, (Hq + 1) * D + 3] = 0xFF80    # -inf in k head 1 of token 2
+    cs = oracle.rope_cos_sin_cache(8192, D, 1_000_000.0)
+    q_want, k_want = oracle.qk_norm_rope_and_cache(qkv, Hq, Hkv, D, wq, wk, 1e-6, cs, pos)
+    t = lambda a: to_torch(a, "bf16", device)  # noqa: E731
+    q, k = ox.qk_norm_rope_and_cache(t(qkv), Hq, Hkv, t(wq), t(wk), 1e-6, torch.from_numpy(cs).to(device),
+                                     torch.from_numpy(pos).to(device), return_k=True)
+    torch.cuda.synchronize()
+    for got, want in ((to_bits(q), q_want), (to_bits(k), k_want)):
+        gf = oracle.half_to_float(got, "bf16")
+        wf = oracle.half_to_float(want, "bf16")
+        assert np.array_equal(np.isnan(gf), np.isnan(wf))
+        fin = ~np.isnan(wf)
+        _assert_ulp(got[fin], want[fin], 0.02)
+    assert np.isnan(oracle.half_to_float(q_want, "bf16")).any()
+
+
+def test_prologue_preallocated_outputs(device):
+    """q_out / k_out: results land in the caller's buffers, identical to fresh ones;
+    wrong shapes are refused."""
+    import torch
+    import oxide_paged_kv as ox
+
+    qkv, wq, wk, pos = _case(13, 7, 8, 2, 128, "bf16", True)
+    cs = torch.from_numpy(oracle.rope_cos_sin_cache(8192, 128, 1_000_000.0)).to(device)
+    t = lambda a: to_torch(a, "bf16", device)  # noqa: E731
+    args = (t(qkv), 8, 2, t(wq), t(wk), 1e-6, cs, torch.from_numpy(pos).to(device))
+    q, k = ox.qk_norm_rope_and_cache(*args, return_k=True)
+    qo = torch.full((7, 8, 128), 7.0, dtype=torch.bfloat16, device=device)
+    ko = torch.full((7, 2, 128), 7.0, dtype=torch.bfloat16, device=device)
+    q2, k2 = ox.qk_norm_rope_and_cache(*args, q_out=qo, k_out=ko)
+    torch.cuda.synchronize()
+    assert q2 is qo and k2 is ko
+    assert torch.equal(qo, q) and torch.equal(ko, k)
+    with pytest.raises(ox.OxideError):
+        ox.qk_norm_rope_and_cache(*args, q_out=torch.empty((7, 8, 64), dtype=torch.bfloat16, device=device))

@@ -69,7 +69,7 @@ def build(verbose: bool = False) -> Path:
 def build_host_test() -> Path:
     """C++ test binary of the host layer (tests/cpp/test_host.cpp), linked to the library."""
     HOST_TEST_BIN.parent.mkdir(parents=True, exist_ok=True)
-    cmd = [HIPCC, *HIP_FLAGS, "-I", str(INCLUDE), "-I", str(HOST), str(HOST_TEST_SRC), "-o",
+    cmd = [HIPCC, *HIP_FLAGS, "-I", str(INCLUDE), "-I", str(HOST), "-I", str(PKG / "csrc"), str(HOST_TEST_SRC), "-o",
            str(HOST_TEST_BIN), "-L", str(PKG), "-loxide_paged_kv", f"-Wl,-rpath,{PKG}",
            "-Wl,-rpath,$ORIGIN/../../../vllm-oxide_amd"]
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -29,6 +29,7 @@
 #include <algorithm>
 
 #include "cdna4_tile.hpp"
+#include "exact_div.hpp"
 #include "oxide_common.hpp"
 
 namespace {
@@ -41,9 +42,22 @@ __device__ __forceinline__ float to_f32(Bf16Tag, uint16_t h) { return __uint_as_
 __device__ __forceinline__ float to_f32(F16Tag, uint16_t h) {
   return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
+// x * w for two 16-bit values widened to fp32 (an exact product).  The empty asm
+// keeps the compiler from fusing the multiply with the following round to f16
+// into v_fma_mix with a +0 addend, which turns a -0 product into +0.
+__device__ __forceinline__ float weigh(float x, float w) {
+  float p = x * w;
+  asm("" : "+v"(p));
+  return p;
+}
+
+// Round a pair to the 16-bit type (nearest even, one packed convert for bf16)
+// and widen it back: the reference's "to dtype" steps between fp32 operations.
 template <class Tag>
-__device__ __forceinline__ float round_to(float x) {
-  return to_f32(Tag{}, pack1(Tag{}, x));
+__device__ __forceinline__ void round_pair(float& a, float& b) {
+  const uint32_t u = pack2(Tag{}, a, b);
+  a = to_f32(Tag{}, static_cast<uint16_t>(u));
+  b = to_f32(Tag{}, static_cast<uint16_t>(u >> 16));
 }
 
 struct RopeParams {
@@ -70,26 +84,35 @@ typedef uint4 vec_t;  // 8 16-bit values
 constexpr int E = 8;   // elements of each half per lane
 
 template <class Tag, int D>
-__device__ __forceinline__ void rope_task(const RopeParams& p, int64_t task, int heads);
+__device__ __forceinline__ void rope_task(const RopeParams& p, int64_t t, int h);
 
 template <class Tag, int D>
 __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_cache_kernel(RopeParams p) {
   const int heads = p.num_heads + 2 * p.num_kv_heads;  // q, k, v heads per token
   constexpr int kTasksPerWg = kRopeThreads / kLanesPerHead<D>;
   const int64_t tasks = p.num_tokens * heads;
-  for (int64_t task = static_cast<int64_t>(blockIdx.x) * kTasksPerWg + threadIdx.x / kLanesPerHead<D>;
-       task < tasks; task += static_cast<int64_t>(gridDim.x) * kTasksPerWg) {
-    rope_task<Tag, D>(p, task, heads);
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kTasksPerWg + threadIdx.x / kLanesPerHead<D>;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kTasksPerWg;
+  const bool narrow = tasks <= INT32_MAX;  // 32-bit token / head split: a 64-bit divide is ~10x the cost
+  for (int64_t task = first; task < tasks; task += stride) {
+    int64_t t;
+    int h;
+    if (narrow) {
+      t = static_cast<uint32_t>(task) / static_cast<uint32_t>(heads);
+      h = static_cast<int>(static_cast<uint32_t>(task) - static_cast<uint32_t>(t) * heads);
+    } else {
+      t = task / heads;
+      h = static_cast<int>(task - t * heads);
+    }
+    rope_task<Tag, D>(p, t, h);
   }
 }
 
 template <class Tag, int D>
-__device__ __forceinline__ void rope_task(const RopeParams& p, int64_t task, int heads) {
+__device__ __forceinline__ void rope_task(const RopeParams& p, int64_t t, int h) {
   // Every product and sum is rounded on its own, as in the reference.
 #pragma clang fp contract(off)
   constexpr int LPH = kLanesPerHead<D>;
-  const int64_t t = task / heads;
-  const int h = static_cast<int>(task % heads);
   const int sub = threadIdx.x % LPH;
   const uint16_t* src = p.qkv + t * p.qkv_stride + static_cast<int64_t>(h) * D;
   const int64_t slot = p.slot_mapping ? p.slot_mapping[t] : -1;
@@ -155,17 +178,44 @@ __device__ __forceinline__ void rope_task(const RopeParams& p, int64_t task, int
 #pragma unroll
     for (int m = 1; m < LPH; m <<= 1) ss = ss + __shfl_xor(ss, m);
     const float sd = sqrtf(ss / static_cast<float>(D) + p.eps);  // correctly rounded / and sqrt
+    // x / sd correctly rounded: three operations per element against the
+    // shared reciprocal where exact_div's domain holds (always, short of
+    // extreme inputs), the general divide otherwise.
+    bool fast = oxide::exact_div_divisor_ok(sd);
 #pragma unroll
-    for (int e = 0; e < E; ++e) {
-      x1[e] = round_to<Tag>(round_to<Tag>(x1[e] / sd) * to_f32(Tag{}, w1[e]));
-      x2[e] = round_to<Tag>(round_to<Tag>(x2[e] / sd) * to_f32(Tag{}, w2[e]));
+    for (int e = 0; e < E; ++e)
+      fast = fast & oxide::exact_div_dividend_ok(x1[e]) & oxide::exact_div_dividend_ok(x2[e]);
+    if (fast) {
+      const float y = 1.0f / sd;
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        x1[e] = oxide::exact_div(x1[e], sd, y);
+        x2[e] = oxide::exact_div(x2[e], sd, y);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        x1[e] = x1[e] / sd;
+        x2[e] = x2[e] / sd;
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < E; e += 2) {
+      round_pair<Tag>(x1[e], x1[e + 1]);
+      round_pair<Tag>(x2[e], x2[e + 1]);
+      x1[e] = weigh(x1[e], to_f32(Tag{}, w1[e]));
+      x1[e + 1] = weigh(x1[e + 1], to_f32(Tag{}, w1[e + 1]));
+      x2[e] = weigh(x2[e], to_f32(Tag{}, w2[e]));
+      x2[e + 1] = weigh(x2[e + 1], to_f32(Tag{}, w2[e + 1]));
+      round_pair<Tag>(x1[e], x1[e + 1]);
+      round_pair<Tag>(x2[e], x2[e + 1]);
     }
   }
-  uint16_t y1[E], y2[E];
+  uint32_t y1[E / 2], y2[E / 2];  // packed pairs
 #pragma unroll
-  for (int e = 0; e < E; ++e) {
-    y1[e] = pack1(Tag{}, x1[e] * c[e] - x2[e] * s[e]);
-    y2[e] = pack1(Tag{}, x2[e] * c[e] + x1[e] * s[e]);
+  for (int e = 0; e < E; e += 2) {
+    y1[e / 2] = pack2(Tag{}, x1[e] * c[e] - x2[e] * s[e], x1[e + 1] * c[e + 1] - x2[e + 1] * s[e + 1]);
+    y2[e / 2] = pack2(Tag{}, x2[e] * c[e] + x1[e] * s[e], x2[e + 1] * c[e + 1] + x1[e + 1] * s[e + 1]);
   }
   uint16_t* dst0;
   uint16_t* dst1 = nullptr;
@@ -187,8 +237,8 @@ __device__ __forceinline__ void rope_task(const RopeParams& p, int64_t task, int
     } else {
 #pragma unroll
       for (int e = 0; e < E; ++e) {
-        dst[sub * E + e] = y1[e];
-        dst[D / 2 + sub * E + e] = y2[e];
+        dst[sub * E + e] = static_cast<uint16_t>(y1[e / 2] >> (16 * (e & 1)));
+        dst[D / 2 + sub * E + e] = static_cast<uint16_t>(y2[e / 2] >> (16 * (e & 1)));
       }
     }
   }

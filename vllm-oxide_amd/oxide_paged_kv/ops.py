@@ -210,12 +210,15 @@ def qk_norm_rope_and_cache(qkv: torch.Tensor, num_heads: int, num_kv_heads: int,
                            q_norm_weight: torch.Tensor | None, k_norm_weight: torch.Tensor | None,
                            eps: float, cos_sin_cache: torch.Tensor, positions: torch.Tensor,
                            key_cache: torch.Tensor | None = None, value_cache: torch.Tensor | None = None,
-                           slot_mapping: torch.Tensor | None = None, return_k: bool = False):
+                           slot_mapping: torch.Tensor | None = None, return_k: bool = False,
+                           q_out: torch.Tensor | None = None, k_out: torch.Tensor | None = None):
     """Qwen3 attention prologue + KV append in one launch (models/qwen3.rs:161-199).
 
     qkv [T, (Hq + 2 Hkv) D] (row = q | k | v); returns q [T, Hq, D] (and k [T, Hkv, D]
     with return_k).  positions int32 [T]; cos_sin_cache fp32 [max_position, D];
     key/value caches [NB, BS, Hkv, D] with int64 slot_mapping [T] (-1 = skip).
+    q_out / k_out: optional preallocated contiguous outputs of those shapes (a
+    serving loop reuses its buffers); k_out implies return_k.
     """
     L = _lib.load()
     T = qkv.shape[0]
@@ -226,8 +229,14 @@ def qk_norm_rope_and_cache(qkv: torch.Tensor, num_heads: int, num_kv_heads: int,
         raise _lib.OxideError("slot_mapping must be int64")
     if qkv.dim() != 2 or qkv.stride(1) != 1:
         raise _lib.OxideError("qkv must be [T, row] with unit element stride")
-    q = torch.empty((T, num_heads, D), dtype=qkv.dtype, device=qkv.device)
-    k = torch.empty((T, num_kv_heads, D), dtype=qkv.dtype, device=qkv.device) if return_k else None
+    for name, t, heads in (("q_out", q_out, num_heads), ("k_out", k_out, num_kv_heads)):
+        if t is not None and (tuple(t.shape) != (T, heads, D) or t.dtype != qkv.dtype
+                              or not t.is_contiguous() or t.device != qkv.device):
+            raise _lib.OxideError(f"{name} must be a contiguous [{T}, {heads}, {D}] tensor like qkv")
+    return_k = return_k or k_out is not None
+    q = q_out if q_out is not None else torch.empty((T, num_heads, D), dtype=qkv.dtype, device=qkv.device)
+    k = k_out if k_out is not None else (
+        torch.empty((T, num_kv_heads, D), dtype=qkv.dtype, device=qkv.device) if return_k else None)
     L.qk_norm_rope_and_cache(_ptr(q), _ptr(k), qkv.data_ptr(), qkv.stride(0), _ptr(q_norm_weight),
                              _ptr(k_norm_weight), float(eps), _ptr(cos_sin_cache), cos_sin_cache.shape[0],
                              _ptr(positions), _ptr(key_cache), _ptr(value_cache), _ptr(slot_mapping), T,
