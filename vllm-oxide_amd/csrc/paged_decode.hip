@@ -302,8 +302,7 @@ __device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* s
         x[j] = (tok >= a && tok < e) ? sc[j] * p.scale_log2 : -INFINITY;
         mt = fmaxf(mt, x[j]);
       }
-      mt = fmaxf(mt, __shfl_xor(mt, 16));
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      mt = max_over_lane_groups(mt);
       const float mnew = fmaxf(m_q, mt);
       const float msafe = mnew == -INFINITY ? 0.f : mnew;
       const float alpha = __builtin_amdgcn_exp2f(m_q - msafe);
@@ -368,8 +367,7 @@ __device__ __forceinline__ void decode_epilogue(const DecodeParams& p, char* sme
   const int qh0 = kh * G;
   // Wave totals: l summed over the 4 lane groups (every group then holds the
   // slot's total); maxima are already equal across groups.
-  l_q += __shfl_xor(l_q, 16);
-  l_q += __shfl_xor(l_q, 32);
+  l_q = sum_over_lane_groups(l_q);
 
   __syncthreads();  // the loop's LDS is reused by the epilogue
   float* s_o = reinterpret_cast<float*>(smem);           // [kWaves][G][D]

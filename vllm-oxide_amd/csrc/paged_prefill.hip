@@ -336,8 +336,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int e = 0; e < 4; ++e) mt = fmaxf(mt, sc[c][kb][e]);
-        mt = fmaxf(mt, __shfl_xor(mt, 16));
-        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        mt = max_over_lane_groups(mt);
         // Lazy rescaling: keep the old maximum while the tile's stays within
         // 2^8 of it (probabilities <= 256, exact in fp32 and bf16 range), so
         // most tiles skip the 32 accumulator multiplies.
