@@ -33,6 +33,33 @@ __device__ __forceinline__ floatx4 mfma16x16x32(F16Tag, uint4 a, uint4 b, floatx
                                                 __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
 }
 
+// 32 x 32 x 16 (gfx950): A lane l holds A[l % 32][8 (l / 32) + i], B lane l holds
+// B[8 (l / 32) + i][l % 32] (i = 0..7), D lane l register r holds
+// D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].  Twice the work of a 16 x 16 x 32
+// per instruction for about the same issue cost, so more VALU work hides
+// behind the matrix pipe.
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+__device__ __forceinline__ floatx16 mfma32x32x16(Bf16Tag, uint4 a, uint4 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+__device__ __forceinline__ floatx16 mfma32x32x16(F16Tag, uint4 a, uint4 b, floatx16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a),
+                                                __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+}
+
+// acc + lo + hi of a packed pair of the MFMA input type (one v_dot2c against 1, 1).
+typedef __bf16 bf16x2_in_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_in_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ float sum2_acc(Bf16Tag, uint32_t packed, float acc) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_in_t, packed),
+                                         __builtin_bit_cast(bf16x2_in_t, 0x3F803F80u), acc, false);
+}
+__device__ __forceinline__ float sum2_acc(F16Tag, uint32_t packed, float acc) {
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_in_t, packed),
+                                __builtin_bit_cast(f16x2_in_t, 0x3C003C00u), acc, false);
+}
+
 // fp32 -> 16-bit storage, round to nearest even.
 __device__ __forceinline__ uint16_t pack1(Bf16Tag, float f) {
   const uint32_t u = __float_as_uint(f);
@@ -85,6 +112,12 @@ __device__ __forceinline__ float max_over_lane_groups(float v) {
   v = fmaxf(v, __shfl_xor(v, 16));
   return fmaxf(v, __shfl_xor(v, 32));
 #endif
+}
+
+// Sum over lanes l and l ^ 32 (the two halves of a 32 x 32 MFMA column).
+__device__ __forceinline__ float sum_over_halves(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ float sum_over_lane_groups(float v) {

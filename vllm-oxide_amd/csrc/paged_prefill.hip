@@ -17,21 +17,23 @@
 // Work split: one workgroup of 4 waves per (128 (token, head) rows of one kv
 // head's group, kv head, sequence).  Row r of the workgroup is token r / G,
 // head r % G of the group, so the G heads that share a kv head share every
-// K/V tile.  Each wave owns 32 rows = two 16-column blocks of the MFMA tiles.
-// K/V advance in 64-key tiles staged through LDS by the whole workgroup with a
-// register prefetch of the next tile and two LDS buffers (one barrier per
-// tile).  Per tile and wave:
-//   * S^T[key][row] = K . Q^T on the matrix cores: A = 16 keys x 32 d from the
-//     K tile (XOR-swizzled 16-byte chunks), B = the rows' queries, held in
-//     registers for the whole kernel.  Lane l gets keys 4(l/16)+j of row l%16.
-//   * online softmax per row in the log2 domain; a row's keys sit in the 4
-//     lane groups of its column, so maxima take two shuffles (xor 16, 32) and
-//     the sums stay per lane until the end.
-//   * O^T[d][row] += V^T . P^T: A = V^T read from the row-major V tile with
-//     the transposing LDS read (keys 4g..4g+3 and 16+4g..16+4g+3 of a 32-key
-//     step), B = the lane's own probabilities in the same key order, so P
-//     never moves between lanes.  Every accumulator of a lane belongs to its
-//     own row: rescaling is a per-lane multiply.
+// K/V tile.  Each wave owns 32 rows, the 32 columns of its MFMA tiles (lanes l
+// and l + 32 share row l % 32).  K/V advance in 64-key tiles loaded straight
+// into LDS by the whole workgroup, two LDS buffers (one barrier per tile).
+// Per tile and wave, with 32 x 32 x 16 MFMAs (half the issue cost per flop of
+// 16 x 16 x 32, so the other wave's softmax work hides behind the matrix pipe):
+//   * S^T[key][row] = K . Q^T: A = 32 keys x 16 d from the K tile (XOR-swizzled
+//     16-byte chunks), B = the rows' queries, held in registers for the whole
+//     kernel.  Lane l gets keys 8(r/4) + 4(l/32) + r%4 of each 32-key block.
+//   * online softmax per row in the log2 domain; a row's keys sit in lanes l
+//     and l ^ 32, so the maximum takes one v_permlane32_swap and the sums stay
+//     per lane until the end.
+//   * O^T[d][row] += V^T . P^T: A = V^T from two transposing LDS reads of the
+//     row-major V tile (keys 16s + 4(l/32) + 0..3 and + 8 of a 32-key block),
+//     B = the lane's own probabilities in the same key order (registers
+//     8s..8s+7 of the score block), so P never moves between lanes.  Every
+//     accumulator of a lane belongs to its own row: rescaling is a per-lane
+//     multiply.
 // Workgroup order is XCD-aware: all row tiles of one (sequence, kv head) run
 // on one XCD (workgroup i runs on XCD i % 8), so its K/V is fetched from HBM
 // once into that XCD's L2 and re-read from there; within a unit the tiles
@@ -81,21 +83,26 @@ __device__ __forceinline__ int clamp_len(int64_t n, int cap) {
 }
 
 // LDS tile layouts (64 keys, row = one key's head slice of 2*D bytes):
-//   K: 16-byte chunk c of row r at chunk position c ^ (r % CH), so the 16 rows
-//      one MFMA operand read touches hit distinct banks;
-//   V: 32-byte granule g of row r at granule position g ^ vswz(r), so the
-//      16 rows x 32 bytes of one transposing read hit distinct banks.
+//   K: 16-byte chunk c of row r at chunk position c ^ kswz(r).  One MFMA
+//      operand read (16 lanes = 16 consecutive rows, one chunk each) then
+//      covers all 64 banks: rows are 256 B apart at D = 128 (kswz = r % 16);
+//      at D = 64 rows r and r + 1 sit in opposite bank halves and
+//      kswz = (r >> 1) % 8 separates the 8 pairs.
+//   V: 32-byte granule g of row r at granule position g ^ vswz(r).  One
+//      transposing read covers 4 consecutive rows x 2 adjacent granules per
+//      half-wave; vswz = 2 (r % 4) at D = 128 (and r & 2 at D = 64, where
+//      odd rows add half a bank sweep) maps those 8 pieces to distinct banks.
 // Both are written by direct global -> LDS loads (global_load_lds_dwordx4):
 // lane i of a wave instruction fills bytes [16 i, 16 i + 16) of a 1 KiB run,
 // so each lane loads the source chunk that belongs at its LDS position.
 template <int D>
-__device__ __forceinline__ int vswz(int r) {
-  return D == 128 ? (r & 7) : ((r >> 1) & 3);
+__device__ __forceinline__ int kswz(int r) {
+  return D == 128 ? (r & 15) : ((r >> 1) & 7);
 }
-
-// 1.0 as a packed pair of the MFMA input type.
-template <class Tag>
-constexpr uint32_t kOnes16 = std::is_same<Tag, Bf16Tag>::value ? 0x3F803F80u : 0x3C003C00u;
+template <int D>
+__device__ __forceinline__ int vswz(int r) {
+  return D == 128 ? 2 * (r & 3) : (r & 2);
+}
 
 // One direct global -> LDS load of 16 bytes per lane: lane i writes LDS bytes
 // [lds + 16 i, lds + 16 i + 16).  Issued as inline assembly so the compiler
@@ -127,8 +134,8 @@ enum PrefillAddressing {
 template <class Tag, int D, int MODE>
 __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParams p) {
   constexpr int CH = D / 8;                  // 16-byte chunks per head row
-  constexpr int KK = D / 32;                 // MFMA k-steps of Q.K
-  constexpr int NDB = D / 16;                // 16-wide d blocks (= 32-byte V granules)
+  constexpr int KS = D / 16;                 // MFMA k-steps of Q.K (16 dims each)
+  constexpr int NDB = D / 32;                // 32-wide d blocks of O (two 32-byte V granules)
   constexpr int ROWB = 2 * D;                // bytes per tile row
   constexpr int TBYTES = kPfKeys * ROWB;     // one K or V tile
   constexpr int BUF = 2 * TBYTES;            // K tile | V tile
@@ -169,24 +176,19 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int r16 = lane & 15;
-  const int grp = lane >> 4;
   const int64_t q0 = p.cu_seqlens_q[b];
   const int rows_used = p.tokens_per_wg * G;
 
-  // This lane's two rows (columns of the MFMA tiles): token, head, key range.
-  int hi_r[2], lo_r[2];
-  int64_t qrow[2];
-  bool valid[2];
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int r = wave * 32 + c * 16 + r16;
-    const int t = t0 + r / G;
-    valid[c] = r < rows_used && t < t1;
-    qrow[c] = valid[c] ? (q0 + t) * p.num_heads + kh * G + r % G : 0;
-    hi_r[c] = valid[c] ? t + off : -1;
-    lo_r[c] = valid[c] && W >= 0 ? t + off - W : 0;
-  }
+  // This lane's row (column l % 32 of the MFMA tiles; lanes l and l + 32 share
+  // it and hold alternate groups of four keys): token, head, key range.
+  const int r32 = lane & 31;
+  const int half = lane >> 5;
+  const int rr = wave * 32 + r32;
+  const int tq = t0 + rr / G;
+  const bool valid = rr < rows_used && tq < t1;
+  const int64_t qrow = valid ? (q0 + tq) * p.num_heads + kh * G + rr % G : 0;
+  const int hi_r = valid ? tq + off : -1;
+  const int lo_r = valid && W >= 0 ? tq + off - W : 0;
   // Key range of the wave's valid rows (wave-uniform) for skipping tiles.
   const int wr0 = wave * 32;
   const int wt_first = t0 + wr0 / G;
@@ -195,11 +197,12 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   const int wave_hi = min(Lk - 1, wt_last + off);
   const int wave_lo = W >= 0 ? wt_first + off - W : 0;
 
-  // Queries (B operand of S^T).  A negative scale is applied as a sign flip of
-  // q (exact) and |scale|, so the running maxima can be taken on raw scores.
+  // Queries (B operand of S^T, 16 dims per k-step).  A negative scale is
+  // applied as a sign flip of q (exact) and |scale|, so the running maxima can
+  // be taken on raw scores.
   const uint32_t qflip = p.scale_log2 < 0.f ? 0x80008000u : 0u;
   const float c_log2 = fabsf(p.scale_log2);
-  uint4 qb[2][KK];  // loaded after the first tile's loads are issued
+  uint4 qb[KS];  // loaded after the first tile's loads are issued
 
   // Direct tile loads: wave w fills tile rows [16 w, 16 w + 16); lane -> (row
   // within the 1 KiB run, 16-byte position), source chunk chosen by the swizzle.
@@ -218,7 +221,7 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
 #pragma unroll
   for (int x = 0; x < NLD; ++x) {
     trow[x] = wave * WROWS + x * RPI + lrow;
-    kchb[x] = 16 * (lpos ^ (trow[x] % CH));
+    kchb[x] = 16 * (lpos ^ kswz<D>(trow[x]));
     vchb[x] = 32 * ((lpos >> 1) ^ vswz<D>(trow[x])) + 16 * (lpos & 1);
     koff[x] = static_cast<uint32_t>(trow[x] * row_stride * 2) + kchb[x];
     voff[x] = static_cast<uint32_t>(trow[x] * row_stride * 2) + vchb[x];
@@ -276,16 +279,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
     }
   };
 
-  float m_r[2] = {-INFINITY, -INFINITY};  // running max of raw scores (x |scale| log2 e)
-  // Row sums of the probabilities on the matrix cores: a ones A operand times
-  // P^T puts the sum over the step's keys of row l%16 in every element.
-  const uint4 ones = make_uint4(kOnes16<Tag>, kOnes16<Tag>, kOnes16<Tag>, kOnes16<Tag>);
-  floatx4 lsum[2] = {floatx4{0.f, 0.f, 0.f, 0.f}, floatx4{0.f, 0.f, 0.f, 0.f}};
-  floatx4 acc[2][NDB];
+  float m_r = -INFINITY;  // running max of raw scores (x |scale| log2 e)
+  // Row sum of the probabilities as rounded for the P.V product (packed
+  // pairs summed by v_dot2c), over this lane's half of the keys.
+  float lsum = 0.f;
+  floatx16 acc[NDB];
 #pragma unroll
-  for (int c = 0; c < 2; ++c)
+  for (int r = 0; r < 16; ++r)
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) acc[c][db] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int db = 0; db < NDB; ++db) acc[db][r] = 0.f;
 
   auto step = [&](int it, char* cur, char* nxt) {
     const int kb0 = kt0 + it * kPfKeys;
@@ -298,94 +300,103 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
       const uint4* sk = reinterpret_cast<const uint4*>(cur);
       const char* sv = cur + TBYTES;
 
-      // Scores of 4 key blocks x 2 row blocks.
-      floatx4 sc[2][4];
+      // S^T of two 32-key blocks: lane l holds keys 8 (r / 4) + 4 half + r % 4
+      // of block kb for its row.
+      floatx16 sc[2];
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        sc[0][kb] = floatx4{0.f, 0.f, 0.f, 0.f};
-        sc[1][kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          const uint4 ka = sk[(kb * 16 + r16) * CH + ((grp + 4 * kk) ^ (r16 % CH))];
-          sc[0][kb] = mfma16x16x32(Tag{}, ka, qb[0][kk], sc[0][kb]);
-          sc[1][kb] = mfma16x16x32(Tag{}, ka, qb[1][kk], sc[1][kb]);
+        for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const uint4 ka = sk[(kb * 32 + r32) * CH + ((2 * ks + half) ^ kswz<D>(r32))];
+          sc[kb] = mfma32x32x16(Tag{}, ka, qb[ks], sc[kb]);
         }
       }
 
       // Mask only where the tile crosses some row's key range.
-      bool lane_mask = false;
+      const bool lane_mask = !(kb0 >= lo_r && kb0 + kPfKeys - 1 <= hi_r);
+      if (__ballot(lane_mask) != 0) {
+        const int k0 = kb0 + 4 * half;
 #pragma unroll
-      for (int c = 0; c < 2; ++c) lane_mask |= !(kb0 >= lo_r[c] && kb0 + kPfKeys - 1 <= hi_r[c]);
-      const bool need_mask = __ballot(lane_mask) != 0;
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int key = k0 + kb * 32 + 8 * (r / 4) + r % 4;
+            sc[kb][r] = (key > hi_r || key < lo_r) ? -INFINITY : sc[kb][r];
+          }
+      }
+      float mt = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mt = fmaxf(mt, sc[kb][r]);
+      {
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mt), __float_as_uint(mt), false, false);
+        const float a = __uint_as_float(sw[0]), b = __uint_as_float(sw[1]);
+        mt = a > b ? a : b;
+      }
+      // Lazy rescaling: keep the old maximum while the tile's stays within
+      // 2^8 of it (probabilities <= 256, exact in fp32 and bf16 range), so
+      // most tiles skip the accumulator multiplies.
+      const float ms = mt * c_log2;
+      const bool grow = ms > m_r + 8.f;
+      float alpha = 1.f;
+      if (grow) {
+        alpha = __builtin_amdgcn_exp2f(m_r - ms);
+        m_r = ms;
+      }
+      if (__ballot(grow) != 0) {
+#pragma unroll
+        for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
+        lsum *= alpha;
+      }
+      const float msafe = m_r == -INFINITY ? 0.f : m_r;
 
+      // P^T: the 8 registers 8 s .. 8 s + 7 of block kb are the B operand of
+      // k-step (kb, s), keys kb * 32 + 16 s + 4 half + {0..3} and + 8 + {0..3}.
       uint4 pb[2][2];
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        if (need_mask) {
-          const int k0 = kb0 + 4 * grp;
+      for (int kb = 0; kb < 2; ++kb) {
+        float x[16];
 #pragma unroll
-          for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const int key = k0 + kb * 16 + e;
-              sc[c][kb][e] = (key > hi_r[c] || key < lo_r[c]) ? -INFINITY : sc[c][kb][e];
-            }
-        }
-        float mt = -INFINITY;
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) mt = fmaxf(mt, sc[c][kb][e]);
-        mt = max_over_lane_groups(mt);
-        // Lazy rescaling: keep the old maximum while the tile's stays within
-        // 2^8 of it (probabilities <= 256, exact in fp32 and bf16 range), so
-        // most tiles skip the 32 accumulator multiplies.
-        const float ms = mt * c_log2;
-        const bool grow = ms > m_r[c] + 8.f;
-        float alpha = 1.f;
-        if (grow) {
-          alpha = __builtin_amdgcn_exp2f(m_r[c] - ms);
-          m_r[c] = ms;
-        }
-        if (__ballot(grow) != 0) {
-#pragma unroll
-          for (int db = 0; db < NDB; ++db) acc[c][db] *= alpha;
-          lsum[c] *= alpha;
-        }
-        const float msafe = m_r[c] == -INFINITY ? 0.f : m_r[c];
-        float x[4][4];
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) x[kb][e] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[c][kb][e], c_log2, -msafe));
+        for (int r = 0; r < 16; ++r) x[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(sc[kb][r], c_log2, -msafe));
 #pragma unroll
         for (int s2 = 0; s2 < 2; ++s2) {
-          pb[c][s2].x = pack2(Tag{}, x[2 * s2][0], x[2 * s2][1]);
-          pb[c][s2].y = pack2(Tag{}, x[2 * s2][2], x[2 * s2][3]);
-          pb[c][s2].z = pack2(Tag{}, x[2 * s2 + 1][0], x[2 * s2 + 1][1]);
-          pb[c][s2].w = pack2(Tag{}, x[2 * s2 + 1][2], x[2 * s2 + 1][3]);
+          pb[kb][s2].x = pack2(Tag{}, x[8 * s2 + 0], x[8 * s2 + 1]);
+          pb[kb][s2].y = pack2(Tag{}, x[8 * s2 + 2], x[8 * s2 + 3]);
+          pb[kb][s2].z = pack2(Tag{}, x[8 * s2 + 4], x[8 * s2 + 5]);
+          pb[kb][s2].w = pack2(Tag{}, x[8 * s2 + 6], x[8 * s2 + 7]);
+          lsum = sum2_acc(Tag{}, pb[kb][s2].x, lsum);
+          lsum = sum2_acc(Tag{}, pb[kb][s2].y, lsum);
+          lsum = sum2_acc(Tag{}, pb[kb][s2].z, lsum);
+          lsum = sum2_acc(Tag{}, pb[kb][s2].w, lsum);
         }
       }
 
-      // O^T += V^T . P^T over two 32-key steps; lane i of group g reads row
-      // 4g + i/4 (+16), logical granule db, bytes 8 (i % 4).
+      // O^T += V^T . P^T: the A operand of d block db for k-step (kb, s) is two
+      // transposing reads; lane i of 16-lane group g reads key row
+      // kb * 32 + 16 s + 4 half + i / 4 (and + 8), 4 dims at
+      // 32 db + 16 (g % 2) + 4 (i % 4), i.e. granule 2 db + g % 2.
+      const int gsub = (lane >> 4) & 1;
+      const int i16 = lane & 15;
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const int rlo = 32 * s2 + 4 * grp + r16 / 4;
-        const char* vlo = sv + rlo * ROWB + 8 * (r16 % 4);
-        const char* vhi = vlo + 16 * ROWB;
-        const int zlo = vswz<D>(rlo), zhi = vswz<D>(rlo + 16);
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int db = 0; db < NDB; ++db) {
-          const uint2 a0 = lds_read_tr16(vlo + 32 * (db ^ zlo));
-          const uint2 a1 = lds_read_tr16(vhi + 32 * (db ^ zhi));
-          const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
-          acc[0][db] = mfma16x16x32(Tag{}, va, pb[0][s2], acc[0][db]);
-          acc[1][db] = mfma16x16x32(Tag{}, va, pb[1][s2], acc[1][db]);
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int rlo = kb * 32 + 16 * s2 + 4 * half + i16 / 4;
+          const char* vlo = sv + rlo * ROWB + 8 * (i16 % 4);
+          const char* vhi = vlo + 8 * ROWB;
+          const int zlo = vswz<D>(rlo), zhi = vswz<D>(rlo + 8);
+#pragma unroll
+          for (int db = 0; db < NDB; ++db) {
+            const int g = 2 * db + gsub;
+            const uint2 a0 = lds_read_tr16(vlo + 32 * (g ^ zlo));
+            const uint2 a1 = lds_read_tr16(vhi + 32 * (g ^ zhi));
+            const uint4 va = make_uint4(a0.x, a0.y, a1.x, a1.y);
+            acc[db] = mfma32x32x16(Tag{}, va, pb[kb][s2], acc[db]);
+          }
         }
-        lsum[0] = mfma16x16x32(Tag{}, ones, pb[0][s2], lsum[0]);
-        lsum[1] = mfma16x16x32(Tag{}, ones, pb[1][s2], lsum[1]);
-      }
     }
     // Block-table entries for the tile after next, once this tile's LDS reads
     // are issued (they complete under the next barrier's wait).
@@ -396,15 +407,15 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
     issue_tile(kt0, smem0);
     if (ntiles > 1) fetch_blocks(kt0 + kPfKeys);
   }
-  // The queries load while the first tile is in flight.
+  // The queries load while the first tile is in flight: k-step ks takes dims
+  // 16 ks + 8 half .. + 7.
+  {
+    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qrow * D;
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const uint16_t* qp = static_cast<const uint16_t*>(p.q) + qrow[c] * D;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      uint4 v = valid[c] ? *reinterpret_cast<const uint4*>(qp + 8 * (grp + 4 * kk)) : make_uint4(0, 0, 0, 0);
+    for (int ks = 0; ks < KS; ++ks) {
+      uint4 v = valid ? *reinterpret_cast<const uint4*>(qp + 16 * ks + 8 * half) : make_uint4(0, 0, 0, 0);
       v.x ^= qflip; v.y ^= qflip; v.z ^= qflip; v.w ^= qflip;
-      qb[c][kk] = v;
+      qb[ks] = v;
     }
   }
 
@@ -413,20 +424,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
     if (it + 1 < ntiles) step(it + 1, smem1, smem0);
   }
 
-  // out[row][d] for d = 16 db + 4 grp + e, normalised by the row total.
-#pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const float l = lsum[c][0];
-    if (!valid[c]) continue;
+  // out[row][d] for d = 32 db + 8 q + 4 half + e (register 4 q + e), normalised
+  // by the row total (both halves of the keys).
+  lsum = sum_over_halves(lsum);
+  if (valid) {
+    const float l = lsum;
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    uint16_t* op = static_cast<uint16_t*>(p.out) + qrow[c] * D + 4 * grp;
+    uint16_t* op = static_cast<uint16_t*>(p.out) + qrow * D + 4 * half;
 #pragma unroll
-    for (int db = 0; db < NDB; ++db) {
-      uint2 w;
-      w.x = pack2(Tag{}, acc[c][db][0] * inv, acc[c][db][1] * inv);
-      w.y = pack2(Tag{}, acc[c][db][2] * inv, acc[c][db][3] * inv);
-      *reinterpret_cast<uint2*>(op + 16 * db) = w;
-    }
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint2 w;
+        w.x = pack2(Tag{}, acc[db][4 * q + 0] * inv, acc[db][4 * q + 1] * inv);
+        w.y = pack2(Tag{}, acc[db][4 * q + 2] * inv, acc[db][4 * q + 3] * inv);
+        *reinterpret_cast<uint2*>(op + 32 * db + 8 * q) = w;
+      }
   }
 }
 
