@@ -51,6 +51,17 @@ def _profile_value(path, key: str):
     return None
 
 
+# Decode pass 1 as reported by split_tokens(): > 0 split grid, 0 persistent, -1 stream.
+PASS1_NAMES = {"split": "split grid", "persistent": "persistent balanced", "stream": "wave-level stream"}
+PASS1_KERNELS = {"split": "paged_decode_split + paged_decode_merge",
+                 "persistent": "paged_decode_persistent + paged_decode_merge_persistent",
+                 "stream": "paged_decode_stream + paged_decode_merge_persistent"}
+
+
+def _pass1(split_tokens: int) -> str:
+    return "split" if split_tokens > 0 else ("persistent" if split_tokens == 0 else "stream")
+
+
 def profiled_traffic(config: int, separate: bool):
     return _profile_value(TRAFFIC_PROFILE.get((config, separate)), "traffic_bytes_per_attention_call")
 
@@ -458,7 +469,7 @@ def main() -> int:
                    "num_kv_heads": H, "head_dim": D, "block_size": BS, "pool_blocks": NB,
                    "ctx": [cfg.ctx_lo, cfg.ctx_hi], "window_left": cfg.window_left,
                    "layers_rotated": layers, "split_tokens": ox.split_tokens(cfg.batch, H, st.max_seqlen_k),
-                   "pass1": "split grid" if ox.split_tokens(cfg.batch, H, st.max_seqlen_k) else "persistent balanced",
+                   "pass1": PASS1_NAMES[_pass1(ox.split_tokens(cfg.batch, H, st.max_seqlen_k))],
                    "total_keys": int(st.context_lens.sum())},
         "step_mode": "separate append + attention" if args.separate else "fused append + attention (one launch)",
         "attn_us": round(attn_us, 2),
@@ -471,9 +482,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": profiled_traffic(args.config, args.separate),
-                     "kernel": ("paged_decode_split + paged_decode_merge"
-                                if ox.split_tokens(cfg.batch, H, st.max_seqlen_k)
-                                else "paged_decode_persistent + paged_decode_merge_persistent")
+                     "kernel": PASS1_KERNELS[_pass1(ox.split_tokens(cfg.batch, H, st.max_seqlen_k))]
                                + " (one attention call" + ("" if args.separate else ", append fused") + ")",
                      "algorithmic_bytes": call_bytes},
         **extra,

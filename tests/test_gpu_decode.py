@@ -68,9 +68,10 @@ CASES = [
 ]
 
 
-@pytest.fixture(params=[1, 2], ids=["split", "persistent"])
+@pytest.fixture(params=[1, 2, 3], ids=["split", "persistent", "stream"])
 def decode_path(request):
-    """Runs a test once per pass-1 path (split grid, persistent balanced pass)."""
+    """Runs a test once per pass-1 path (split grid, persistent balanced pass,
+    wave-level stream pass)."""
     import oxide_paged_kv as ox
 
     ox.set_decode_path(request.param)
@@ -265,23 +266,32 @@ def test_decode_cfg4_prefix_cow_window_full_size(device):
 
 
 def test_decode_path_policy(device):
-    """Long contexts take the persistent balanced pass (split_tokens 0), the others a
-    split grid; cfg5 and cfg3 shapes."""
+    """Shapes with >= ~1024 keys per stream range take the wave-level stream pass
+    (split_tokens -1: cfg5, cfg3, cfg4), smaller ones a split grid (cfg2); kv head
+    counts that do not divide 8 take the persistent pass when long (split_tokens 0)."""
     import oxide_paged_kv as ox
 
-    assert ox.split_tokens(16, 8, 131072) == 0
+    assert ox.split_tokens(16, 8, 131072) == -1
+    assert ox.split_tokens(64, 8, 8192) == -1
+    assert ox.split_tokens(128, 8, 5120) == -1
+    assert ox.split_tokens(32, 8, 4096) == 256
+    assert ox.split_tokens(16, 16, 131072) == 0
+    ox.set_decode_path(1)
     assert ox.split_tokens(64, 8, 8192) == 1024
+    ox.set_decode_path(0)
     ox.set_decode_path(1)
     assert ox.split_tokens(16, 8, 131072) == 1024
     ox.set_decode_path(2)
     assert ox.split_tokens(64, 8, 8192) == 0
+    ox.set_decode_path(3)
+    assert ox.split_tokens(64, 8, 8192) == -1
     ox.set_decode_path(0)
 
 
 @pytest.mark.parametrize("cfg_id", [3, 5])
 def test_decode_paths_agree_full_size(device, cfg_id):
-    """Full-size cfg3 / cfg5 through both passes: outputs agree within rounding of
-    the partial merges (max-abs 2e-2, the attention tolerance)."""
+    """Full-size cfg3 / cfg5 through all three pass-1 paths: outputs agree within
+    rounding of the partial merges (max-abs 2e-2, the attention tolerance)."""
     import torch
     import oxide_paged_kv as ox
 
@@ -291,15 +301,17 @@ def test_decode_paths_agree_full_size(device, cfg_id):
     bt = torch.from_numpy(st.block_table).to(device)
     outs = []
     try:
-        for path in (1, 2):
+        for path in (1, 2, 3):
             ox.set_decode_path(path)
             print(f"cfg{cfg_id} path {path}", flush=True)
             outs.append(to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim))))
     finally:
         ox.set_decode_path(0)
     assert_attn_close(outs[1], outs[0])
+    assert_attn_close(outs[2], outs[0])
     lens = st.context_lens.astype(np.int64)
-    _check_sampled(st, kc, vc, q, outs[1], [int(lens.argmax()), int(lens.argmin())])
+    for o in outs[1:]:
+        _check_sampled(st, kc, vc, q, o, [int(lens.argmax()), int(lens.argmin())])
 
 
 def test_decode_cfg5_long_context_full_size(device):
@@ -320,15 +332,15 @@ def test_decode_cfg5_long_context_full_size(device):
 
 @pytest.mark.parametrize("batch,ctx_hi,want_split", [(64, 4096, 512), (64, 8192, 1024), (8, 3000, 256)])
 def test_decode_each_split_size_sampled(device, batch, ctx_hi, want_split):
-    """One batch per split size the policy picks (256, 512 and 1024 keys per
-    workgroup), Qwen3-8B heads, sampled sequences checked against the oracle."""
+    """One batch per split size the split grid picks (256, 512 and 1024 keys per
+    workgroup; the split path is forced, the shape policy may prefer the stream
+    pass), Qwen3-8B heads, sampled sequences checked against the oracle."""
     import torch
     import oxide_paged_kv as ox
     from oxide_paged_kv.workload import DecodeConfig, make_decode_step
 
     cfg = DecodeConfig(f"split{want_split}", 32, 8, 128, batch, 1, ctx_hi, 0)
     st = make_decode_step(cfg, seed=want_split)
-    assert ox.split_tokens(batch, 8, st.max_seqlen_k) == want_split
     g = torch.Generator(device=device).manual_seed(want_split)
     shape = (st.pool_blocks, 256, 8, 128)
     kc = torch.randn(shape, generator=g, device=device).bfloat16()
@@ -336,7 +348,12 @@ def test_decode_each_split_size_sampled(device, batch, ctx_hi, want_split):
     q = torch.randn((batch, 32, 128), generator=g, device=device).bfloat16()
     cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
     bt = torch.from_numpy(st.block_table).to(device)
-    out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(128)))
+    ox.set_decode_path(1)
+    try:
+        assert ox.split_tokens(batch, 8, st.max_seqlen_k) == want_split
+        out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(128)))
+    finally:
+        ox.set_decode_path(0)
     lens = st.context_lens.astype(np.int64)
     _check_sampled(st, kc, vc, q, out, sorted({0, int(lens.argmax()), int(lens.argmin()), batch - 1}))
 

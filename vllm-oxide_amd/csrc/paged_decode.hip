@@ -201,14 +201,48 @@ __device__ __forceinline__ void load_q(const DecodeParams& p, int b, int kh, uin
   for (int kk = 0; kk < D / 32; ++kk) qb[kk] = *reinterpret_cast<const uint4*>(qrow + 8 * ((lane >> 4) + 4 * kk));
 }
 
-// One wave's pass over the TILES 16-key tiles from key w0, restricted to keys
-// [a, e) (a < e): updates the running max / partial sum of query slot lane % 16
-// and the PV accumulators.  L is the sequence length (the fused append owns key
-// L - 1).
+// A 16-key tile to load ahead: kv head kh of sequence b, keys tt .. tt + 15
+// (tt 16-aligned and inside the sequence).
+struct NextTile {
+  bool valid;
+  int b, kh, tt;
+};
+
+// K/V rows of tile tt of (b, kh) into registers: lane l loads 16-byte chunk
+// l % CH of rows l / CH + RPL j.
+template <int D, int G, int TILES>
+__device__ __forceinline__ void load_tile_rows(const DecodeParams& p, int b, int kh, int tt,
+                                               uint4 (&kr)[SplitShape<D, G, TILES>::VL],
+                                               uint4 (&vr)[SplitShape<D, G, TILES>::VL]) {
+  typedef SplitShape<D, G, TILES> S;
+  const int lane = threadIdx.x & 63;
+  const int vch = lane % S::CH;
+  const int vrow = lane / S::CH;
+  const int BS = p.block_size;
+  const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
+  const int32_t* bt = p.block_table + b * p.max_blocks;
+  const int blk = min(max(bt[tt / BS], 0), p.num_blocks - 1);
+  const int64_t row0 = static_cast<int64_t>(blk) * BS + tt % BS;
+  const uint16_t* kp = static_cast<const uint16_t*>(p.k) + kh * D + (row0 + vrow) * row_stride + 8 * vch;
+  const uint16_t* vp = static_cast<const uint16_t*>(p.v) + kh * D + (row0 + vrow) * row_stride + 8 * vch;
+#pragma unroll
+  for (int j = 0; j < S::VL; ++j) kr[j] = load_kv16(kp + S::RPL * j * row_stride);
+#pragma unroll
+  for (int j = 0; j < S::VL; ++j) vr[j] = load_kv16(vp + S::RPL * j * row_stride);
+}
+
+// The same as decode_wave_tiles below with the register double buffer held by
+// the caller: with `preloaded` the first tile is already in buffer 0, and
+// with nx.valid the last step loads tile nx into buffer 0 for the caller's
+// next call (TILES is even), so a wave streams block after block without
+// waiting on a fresh first load.
 template <class Tag, int D, int G, int TILES>
-__device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* smem, int b, int kh, int L,
-                                                  int w0, int a, int e, const uint4 (&qb)[D / 32],
-                                                  float& m_q, float& l_q, floatx4 (&acc)[D / 16]) {
+__device__ __forceinline__ void decode_wave_tiles_buf(const DecodeParams& p, char* smem, int b, int kh, int L,
+                                                      int w0, int a, int e, const uint4 (&qb)[D / 32],
+                                                      float& m_q, float& l_q, floatx4 (&acc)[D / 16],
+                                                      uint4 (&kst)[2][SplitShape<D, G, TILES>::VL],
+                                                      uint4 (&vst)[2][SplitShape<D, G, TILES>::VL],
+                                                      bool preloaded, const NextTile& nx, int64_t slot_new) {
   typedef SplitShape<D, G, TILES> S;
   constexpr int KK = S::KK, CH = S::CH, RPL = S::RPL, VL = S::VL, NDT = S::NDT, VRS = S::VRS;
   const int wave = threadIdx.x >> 6;
@@ -227,7 +261,6 @@ __device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* s
   {
     const int first_tile = a & ~15;
     const int last_tile = (e - 1) & ~15;
-    uint4 kst[2][VL], vst[2][VL];
     auto load_tile = [&](int t, uint4 (&kr)[VL], uint4 (&vr)[VL]) {
       const int tt = __builtin_amdgcn_readfirstlane(min(max(w0 + 16 * t, first_tile), last_tile));
       const int blk = min(max(bt[tt / BS], 0), p.num_blocks - 1);
@@ -244,17 +277,19 @@ __device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* s
     // writes this kv head's slice of the token's K/V row to its slot and uses
     // it in place of the row it loaded from the cache.  No other workgroup
     // reads that slice, so no ordering with other workgroups is needed.
+    // slot_new: the new token's slot (fused append, read by the caller), or -1.
     const int key_new = L - 1;
-    int64_t slot_new = -1;
-    if (p.new_k != nullptr) slot_new = p.slot_mapping[b];
     const bool owns_new = slot_new >= 0 && key_new >= a && key_new < e;
 
     float p_even[4] = {0.f, 0.f, 0.f, 0.f};
     float alpha_even = 1.f;
-    load_tile(0, kst[0], vst[0]);
+    if (!preloaded) load_tile(0, kst[0], vst[0]);
 #pragma unroll
     for (int t = 0; t < TILES; ++t) {
-      if (t + 1 < TILES) load_tile(t + 1, kst[(t + 1) & 1], vst[(t + 1) & 1]);
+      if (t + 1 < TILES)
+        load_tile(t + 1, kst[(t + 1) & 1], vst[(t + 1) & 1]);
+      else if (nx.valid)
+        load_tile_rows<D, G, TILES>(p, nx.b, nx.kh, nx.tt, kst[(t + 1) & 1], vst[(t + 1) & 1]);
       const uint4(&kr)[VL] = kst[t & 1];
       const uint4(&vr)[VL] = vst[t & 1];
       const int tt = w0 + 16 * t;
@@ -349,6 +384,21 @@ __device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* s
     }
   }
 
+}
+
+// One wave's pass over the TILES 16-key tiles from key w0, restricted to keys
+// [a, e) (a < e): updates the running max / partial sum of query slot lane % 16
+// and the PV accumulators.  L is the sequence length (the fused append owns key
+// L - 1).
+template <class Tag, int D, int G, int TILES>
+__device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* smem, int b, int kh, int L,
+                                                  int w0, int a, int e, const uint4 (&qb)[D / 32],
+                                                  float& m_q, float& l_q, floatx4 (&acc)[D / 16]) {
+  uint4 kst[2][SplitShape<D, G, TILES>::VL], vst[2][SplitShape<D, G, TILES>::VL];
+  const NextTile none{false, 0, 0, 0};
+  const int64_t slot_new = p.new_k != nullptr ? p.slot_mapping[b] : -1;
+  decode_wave_tiles_buf<Tag, D, G, TILES>(p, smem, b, kh, L, w0, a, e, qb, m_q, l_q, acc, kst, vst, false, none,
+                                          slot_new);
 }
 
 // Merges the 4 waves' states through LDS and writes, per query q of the group,
@@ -537,6 +587,152 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_persistent(DecodePar
   }
 }
 
+// ---------------------------------------------------------------------------
+// Wave-level balanced pass 1 (stream).  A workgroup is 8 waves (one per CU):
+// wave i takes kv head i % Hkv, so the Hkv waves reading one key range fetch
+// the same cache rows (all heads of a key sit in one 2*Hkv*D-byte row) at the
+// same time -- reading each head's range at a different time costs 5-8 % of
+// the achievable HBM rate on MI355X.  The keys of the batch are laid end to
+// end (key j of sequence b at cu_seqlens_k[b] + j) and cut into U = W * P
+// ranges, P = 8 / Hkv; unit u = w * P + i / Hkv of workgroup w takes keys
+// [u K / U, (u+1) K / U) of its head.  A wave streams its range without any
+// barrier: sequence after sequence, in 256-key blocks and 32-key blocks for a
+// sequence's last keys, with the register double buffer carried across blocks
+// and sequences (the next block's first tile is in flight while the current
+// block's last tile computes).  No workgroup turns over, no wave waits for
+// another, no cross-wave merge: a sequence wholly inside the range writes its
+// output from registers; a piece writes a partial to slot (u, kh, 0) (the
+// range's first sequence) or (u, kh, 1) (its last), and pass 2
+// (paged_decode_merge_persistent<.., true>) combines the pieces.
+constexpr int kStreamWaves = 8;
+
+// Per-wave epilogue of a segment: query slot s < G of lane group 0 holds
+// query s; acc[dt][j] of lane l is slot 4 (l / 16) + j, dim 16 dt + l % 16.
+template <class Tag, int D, int G>
+__device__ __forceinline__ void decode_wave_epilogue(const DecodeParams& p, int b, int kh, float m_q, float l_q,
+                                                     const floatx4 (&acc)[D / 16], bool direct,
+                                                     int64_t prow_base) {
+  constexpr int NDT = D / 16;
+  const int lane = threadIdx.x & 63;
+  const int r16 = lane & 15;
+  const int grp = lane >> 4;
+  l_q = sum_over_lane_groups(l_q);
+  uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + kh * G) * D;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int slot = 4 * grp + j;
+    const float l = __shfl(l_q, slot);
+    const float m = __shfl(m_q, slot);
+    if (slot < G) {
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      if (direct) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) out[slot * D + dt * 16 + r16] = pack1(Tag{}, acc[dt][j] * inv);
+      } else {
+        const int64_t prow = prow_base + slot;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) p.part_o[prow * D + dt * 16 + r16] = acc[dt][j] * inv;
+        if (r16 == 0) p.part_lse[prow] = l > 0.f ? m + log2f(l) : -INFINITY;
+      }
+    }
+  }
+}
+
+template <class Tag, int D, int G>
+__global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(DecodeParams p) {
+  typedef SplitShape<D, G, 16> S16;
+  typedef SplitShape<D, G, 2> S2;
+  static_assert(S16::VL == S2::VL && S16::WAVE_BYTES == S2::WAVE_BYTES, "tile shapes shared by both block sizes");
+  __shared__ __align__(16) char smem[kStreamWaves * S16::WAVE_BYTES];
+  const int Hkv = p.num_kv_heads;  // divides 8 (checked on the host)
+  const int P = kStreamWaves / Hkv;
+  const int U = p.num_wgs;         // key ranges per head: gridDim.x * P
+  const int W = gridDim.x;
+  // Workgroup i runs on XCD i % 8: each XCD holds a contiguous eighth of the
+  // ranges (W is a multiple of 8).  Everything below is wave-uniform.
+  const int wg = (blockIdx.x % kXcds) * (W / kXcds) + blockIdx.x / kXcds;
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kh = wv % Hkv;
+  const int u = wg * P + wv / Hkv;
+  const int64_t K = p.cu_seqlens_k[p.batch];
+  const int64_t R0 = static_cast<int64_t>(u) * K / U;
+  const int64_t R1 = static_cast<int64_t>(u + 1) * K / U;
+  if (R0 >= R1) return;  // no barrier anywhere in this kernel: waves may leave alone
+  // The tile helpers use LDS area threadIdx.x / 64 of smem (8 areas here).
+
+  // Sequence iterator over the range: keys [j0, j1) of sequence b, attended
+  // keys [a, e) among them.
+  struct Seg {
+    bool valid;
+    int b, L, j0, j1, a, e;
+    bool whole;
+  };
+  auto seg_at = [&](int64_t x, int bb) -> Seg {
+    Seg g{false, 0, 0, 0, 0, 0, 0, false};
+    while (x < R1 && bb < p.batch) {
+      const int64_t cb = p.cu_seqlens_k[bb];
+      const int64_t Lraw = max(static_cast<int64_t>(p.cu_seqlens_k[bb + 1]) - cb, int64_t{0});
+      if (x < cb) x = cb;  // only with a decreasing cu_seqlens_k
+      if (x >= R1) break;
+      if (x >= cb + Lraw) {
+        ++bb;
+        continue;
+      }
+      const int j0 = static_cast<int>(x - cb);
+      const int j1 = static_cast<int>(min(R1, cb + Lraw) - cb);
+      const int L = seq_len(p, bb);
+      const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
+      g = Seg{true, bb, L, j0, j1, max(j0, lo), min(j1, L), j0 == 0 && j1 == Lraw};
+      break;
+    }
+    return g;
+  };
+  auto first_tile = [&](const Seg& g) -> NextTile {
+    return g.valid && g.a < g.e ? NextTile{true, g.b, kh, g.a & ~15} : NextTile{false, 0, 0, 0};
+  };
+
+  uint4 kst[2][S16::VL], vst[2][S16::VL];
+  Seg cur = seg_at(R0, find_seq(p.cu_seqlens_k, p.batch, R0));
+  bool first_seg = true;
+  bool preloaded = false;
+  while (cur.valid) {
+    const Seg nxt = seg_at(p.cu_seqlens_k[cur.b] + static_cast<int64_t>(cur.j1), cur.b);
+    float m_q = -INFINITY, l_q = 0.f;
+    floatx4 acc[S16::NDT];
+#pragma unroll
+    for (int dt = 0; dt < S16::NDT; ++dt) acc[dt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (cur.a < cur.e) {
+      uint4 qb[S16::KK];
+      load_q<D, G>(p, cur.b, kh, qb);
+      // Fused append: only the piece holding key L - 1 needs the slot.
+      const int64_t slot_new =
+          p.new_k != nullptr && cur.a <= cur.L - 1 && cur.L - 1 < cur.e ? p.slot_mapping[cur.b] : -1;
+      int blk0 = cur.a & ~15;
+      int ntiles = ((cur.e - 1) & ~15) / 16 - blk0 / 16 + 1;
+      while (ntiles > 0) {
+        const bool big = ntiles >= 16;
+        const int step = big ? 16 : 2;
+        const NextTile nt = ntiles > step ? NextTile{true, cur.b, kh, blk0 + 16 * step} : first_tile(nxt);
+        const int a = max(cur.a, blk0);
+        const int e = min(cur.e, blk0 + 16 * step);
+        if (big)
+          decode_wave_tiles_buf<Tag, D, G, 16>(p, smem, cur.b, kh, cur.L, blk0, a, e, qb, m_q, l_q, acc, kst, vst,
+                                                preloaded, nt, slot_new);
+        else
+          decode_wave_tiles_buf<Tag, D, G, 2>(p, smem, cur.b, kh, cur.L, blk0, a, e, qb, m_q, l_q, acc, kst, vst,
+                                               preloaded, nt, slot_new);
+        preloaded = nt.valid;
+        blk0 += 16 * step;
+        ntiles -= step;
+      }
+    }
+    decode_wave_epilogue<Tag, D, G>(p, cur.b, kh, m_q, l_q, acc, cur.whole,
+                                    ((static_cast<int64_t>(u) * Hkv + kh) * 2 + (first_seg ? 0 : 1)) * G);
+    first_seg = false;
+    cur = nxt;
+  }
+}
+
 // Pass 2: one workgroup of 4 waves per (query head, sequence) merges the
 // splits that intersect [lo, L) with log-sum-exp weights; each wave takes a
 // contiguous quarter of the splits and the quarters are combined in LDS.
@@ -640,10 +836,13 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge(DecodeParams p) {
   }
 }
 
-// Pass 2 of the persistent path: per (query head, sequence), the pieces of
-// its (b, kh) from workgroups owner(g0) .. owner(g0 + L - 1), combined with
-// log-sum-exp weights (a piece outside the window has weight 0).
-template <class Tag, int D>
+// Pass 2 of the balanced paths: per (query head, sequence), the pieces of its
+// (b, kh) from range owners owner(g0) .. owner(g0 + L - 1), combined with
+// log-sum-exp weights (a piece outside the window has weight 0).  Persistent:
+// owners are workgroups over positions g = Hkv cu[b] + kh L_b + j, rows
+// (w * 2 + slot) * G + q.  Stream: owners are per-head key ranges over
+// g = cu[b] + j, rows ((u * Hkv + kh) * 2 + slot) * G + q.
+template <class Tag, int D, bool STREAM = false>
 __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(DecodeParams p) {
   constexpr int PER = D / 64;
   __shared__ float s_o[kWaves][D];
@@ -676,8 +875,9 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(Decode
     return;
   }
   const int W = p.num_wgs;
-  const int64_t N = static_cast<int64_t>(p.num_kv_heads) * p.cu_seqlens_k[p.batch];
-  const int64_t g0 = static_cast<int64_t>(p.num_kv_heads) * cb + kh * Lraw;
+  const int64_t N = STREAM ? static_cast<int64_t>(p.cu_seqlens_k[p.batch])
+                           : static_cast<int64_t>(p.num_kv_heads) * p.cu_seqlens_k[p.batch];
+  const int64_t g0 = STREAM ? cb : static_cast<int64_t>(p.num_kv_heads) * cb + kh * Lraw;
   if (g0 + Lraw > N) {  // inconsistent cu_seqlens_k: pass 1 did not cover these keys
     for (int i = threadIdx.x; i < D; i += kThreads) out[i] = 0;
     return;
@@ -686,7 +886,10 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(Decode
   const int64_t wb = owner_wg(g0 + Lraw - 1, N, W);
   if (wa == wb) return;  // one workgroup held all of it and wrote the output
   const int s_first = wa * N / W < g0 ? 1 : 0;
-  auto row = [&](int i) -> int64_t { return ((wa + i) * 2 + (i == 0 ? s_first : 0)) * G + q; };
+  auto row = [&](int i) -> int64_t {
+    const int64_t owner = STREAM ? (wa + i) * p.num_kv_heads + kh : wa + i;
+    return (owner * 2 + (i == 0 ? s_first : 0)) * G + q;
+  };
   // With fewer positions than workgroups some own an empty range and wrote
   // nothing: their slots are skipped.
   auto piece_lse = [&](int i) -> float {
@@ -775,11 +978,31 @@ int device_cu_count();
 // B=16 ctx 32k-128k: 883 vs 953 us); slower below (Qwen3-8B B=64 ctx 2k-8k,
 // Qwen3-0.6B B=32 ctx 0.5k-4k), where the split grid's many short workgroups
 // hide their start-up and the XCD-aware order helps more than the balance.
-bool use_persistent(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
+enum DecodePath { kPathSplit = 1, kPathPersistent = 2, kPathStream = 3 };
+
+// The stream pass needs the kv heads to divide its 8 waves per workgroup.
+bool stream_ok(int64_t num_kv_heads) { return num_kv_heads >= 1 && num_kv_heads <= 8 && 8 % num_kv_heads == 0; }
+
+// Path by shape (measured on MI355X, K/V read rate against the 8 TB/s peak):
+//   * stream when each of its key ranges holds >= ~1024 keys at the longest
+//     (batch * max_seqlen_k / (CUs * 8 / Hkv)): Qwen3-8B B=64 ctx 2k-8k 74.7 %
+//     (split 72.0 %), B=128 shared prefix + window 86.4 % (split 81.9 %),
+//     Qwen3-32B B=16 ctx 32k-128k 79.9 % (persistent 77.7 %);
+//   * below that the split grid (Qwen3-0.6B B=32 ctx 0.5k-4k: split 64 %,
+//     stream 54 %: ranges of ~300 keys make the merge and the per-sequence
+//     start-up dominate);
+//   * kv head counts that do not divide 8 take the persistent pass for long
+//     shapes, the split grid otherwise.
+DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
   const int forced = g_decode_path.load(std::memory_order_relaxed);
-  if (forced == 1) return false;
-  if (forced == 2) return true;
-  return batch * max_seqlen_k * num_kv_heads >= int64_t{16384} * 2 * device_cu_count();
+  if (forced == kPathStream && !stream_ok(num_kv_heads)) return kPathPersistent;
+  if (forced >= kPathSplit && forced <= kPathStream) return static_cast<DecodePath>(forced);
+  const int64_t cus = device_cu_count();
+  if (stream_ok(num_kv_heads)) {
+    const int64_t ranges = cus * (8 / num_kv_heads);
+    return batch * max_seqlen_k >= int64_t{1024} * ranges ? kPathStream : kPathSplit;
+  }
+  return batch * max_seqlen_k * num_kv_heads >= int64_t{16384} * 2 * cus ? kPathPersistent : kPathSplit;
 }
 
 int64_t choose_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
@@ -900,6 +1123,35 @@ bool dispatch_persistent(const DecodeParams& p, int group, hipStream_t s) {
   }
 }
 
+template <class Tag, int D, int G>
+void launch_stream(DecodeParams p, hipStream_t s) {
+  // One workgroup of 8 waves per CU; 8 / Hkv key ranges per workgroup and head.
+  int wgs = device_cu_count();
+  wgs -= wgs % kXcds;  // a whole number of workgroups per XCD
+  p.num_wgs = wgs * (kStreamWaves / p.num_kv_heads);
+  hipLaunchKernelGGL((paged_decode_stream<Tag, D, G>), dim3(static_cast<unsigned>(wgs)), dim3(64 * kStreamWaves), 0,
+                     s, p);
+  hipLaunchKernelGGL((paged_decode_merge_persistent<Tag, D, true>),
+                     dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(kThreads),
+                     0, s, p);
+}
+
+template <class Tag, int D>
+bool dispatch_stream(const DecodeParams& p, int group, hipStream_t s) {
+  switch (group) {
+    case 1: launch_stream<Tag, D, 1>(p, s); return true;
+    case 2: launch_stream<Tag, D, 2>(p, s); return true;
+    case 3: launch_stream<Tag, D, 3>(p, s); return true;
+    case 4: launch_stream<Tag, D, 4>(p, s); return true;
+    case 5: launch_stream<Tag, D, 5>(p, s); return true;
+    case 6: launch_stream<Tag, D, 6>(p, s); return true;
+    case 7: launch_stream<Tag, D, 7>(p, s); return true;
+    case 8: launch_stream<Tag, D, 8>(p, s); return true;
+    case 16: launch_stream<Tag, D, 16>(p, s); return true;
+    default: return false;
+  }
+}
+
 template <class Tag>
 bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hipStream_t s) {
   if (p.max_splits == 0) {
@@ -912,6 +1164,11 @@ bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hip
   if (p.split_tokens == 0) {
     if (head_dim == 128) return dispatch_persistent<Tag, 128>(p, group, s);
     if (head_dim == 64) return dispatch_persistent<Tag, 64>(p, group, s);
+    return false;
+  }
+  if (p.split_tokens < 0) {
+    if (head_dim == 128) return dispatch_stream<Tag, 128>(p, group, s);
+    if (head_dim == 64) return dispatch_stream<Tag, 64>(p, group, s);
     return false;
   }
   const dim3 mgrid(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(batch));
@@ -943,20 +1200,27 @@ WorkspaceLayout workspace_layout(int64_t rows, int64_t head_dim) {
 int64_t split_rows(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t max_seqlen_k) {
   return batch * num_heads * ceil_div(max_seqlen_k, choose_split_tokens(batch, num_kv_heads, max_seqlen_k));
 }
+// Balanced paths: two rows per range owner and query of the group; owners
+// are workgroups (persistent, up to kMaxWgsPerCu per CU) or waves (stream, up
+// to 2 workgroups of kWaves per CU).
 int64_t persistent_rows(int64_t num_heads, int64_t num_kv_heads) {
-  return 2 * static_cast<int64_t>(device_cu_count()) * kMaxWgsPerCu * (num_heads / num_kv_heads);
+  return 2 * static_cast<int64_t>(device_cu_count()) * std::max(kMaxWgsPerCu, 2 * kWaves) *
+         (num_heads / num_kv_heads);
 }
 
 }  // namespace
 
 extern "C" int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
                                                        int64_t max_seqlen_k) {
-  return use_persistent(batch, num_kv_heads, max_seqlen_k) ? 0
-                                                           : choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
+  switch (choose_path(batch, num_kv_heads, max_seqlen_k)) {
+    case kPathPersistent: return 0;
+    case kPathStream: return -1;
+    default: return choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
+  }
 }
 
 extern "C" void oxide_set_decode_path(int path) {
-  g_decode_path.store(path == 1 || path == 2 ? path : 0, std::memory_order_relaxed);
+  g_decode_path.store(path >= 1 && path <= 3 ? path : 0, std::memory_order_relaxed);
 }
 
 extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
@@ -1012,7 +1276,8 @@ void decode_attention_impl(void* out, const void* q, const void* new_k, const vo
     return;
   }
   DecodeParams p{};
-  const bool persistent = max_seqlen_k > 0 && use_persistent(batch, num_kv_heads, max_seqlen_k);
+  const DecodePath path = max_seqlen_k > 0 ? choose_path(batch, num_kv_heads, max_seqlen_k) : kPathSplit;
+  const bool persistent = path != kPathSplit;
   const int64_t st = max_seqlen_k > 0 ? choose_split_tokens(batch, num_kv_heads, max_seqlen_k) : 1;
   const int64_t max_splits = max_seqlen_k > 0 ? ceil_div(max_seqlen_k, st) : 0;
   const WorkspaceLayout wl = workspace_layout(
@@ -1036,7 +1301,8 @@ void decode_attention_impl(void* out, const void* q, const void* new_k, const vo
   p.num_kv_heads = static_cast<int>(num_kv_heads);
   p.block_size = static_cast<int>(page_block_size);
   p.window_left = window_left < 0 ? -1 : window_left;
-  p.split_tokens = persistent ? 0 : static_cast<int>(st);  // 0 selects the persistent path
+  // 0 selects the persistent path, -1 the stream path.
+  p.split_tokens = path == kPathPersistent ? 0 : path == kPathStream ? -1 : static_cast<int>(st);
   p.max_splits = static_cast<int>(max_splits);
   p.batch = static_cast<int>(batch);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;

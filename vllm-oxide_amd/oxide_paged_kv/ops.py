@@ -97,12 +97,14 @@ def workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
 
 
 def split_tokens(batch: int, num_kv_heads: int, max_seqlen_k: int) -> int:
-    """Tokens per KV split of the decode pass 1, or 0 for the persistent balanced pass."""
+    """Tokens per KV split of the decode pass 1; 0 for the persistent balanced pass, -1 for
+    the wave-level stream pass."""
     return int(_lib.load().paged_decode_attention_split_tokens(batch, num_kv_heads, max_seqlen_k))
 
 
 def set_decode_path(path: int) -> None:
-    """0 = choose by shape, 1 = split grid, 2 = persistent balanced pass (process-wide)."""
+    """0 = choose by shape, 1 = split grid, 2 = persistent balanced pass, 3 = wave-level
+    stream pass (process-wide)."""
     _lib.load().oxide_set_decode_path(int(path))
 
 
