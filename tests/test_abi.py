@@ -68,15 +68,26 @@ def test_error_paths_without_launch():
 
 
 def test_workspace_and_split_policy():
+    """Long shapes take the stream pass (-1), small ones a split grid; the workspace
+    holds either path's partials (split: a row per (sequence, head, split); stream:
+    two per (key range, kv head, query of the group), 8 ranges per CU per head set;
+    without a GPU the CU count reads as 256)."""
     import oxide_paged_kv as ox
 
-    st = ox.split_tokens(64, 8, 8192)
-    assert st % 256 == 0
-    ws = ox.workspace_size(64, 32, 8, 128, 8192)
-    splits = -(-8192 // st)
-    assert ws >= 64 * 32 * splits * (128 + 1) * 4
-    assert ox.workspace_size(64, 32, 8, 128, 0) == 0
+    assert ox.split_tokens(64, 8, 8192) == -1
+    assert ox.split_tokens(32, 8, 4096) == 256
     assert ox.split_tokens(1, 1, 100) == 256
+    ws = ox.workspace_size(64, 32, 8, 128, 8192)
+    assert ws >= 2 * 256 * 8 * 4 * (128 + 1) * 4
+    ox.set_decode_path(1)
+    try:
+        st = ox.split_tokens(64, 8, 8192)
+        assert st % 256 == 0
+        splits = -(-8192 // st)
+        assert ox.workspace_size(64, 32, 8, 128, 8192) >= 64 * 32 * splits * (128 + 1) * 4
+    finally:
+        ox.set_decode_path(0)
+    assert ox.workspace_size(64, 32, 8, 128, 0) == 0
 
 
 def test_no_cpu_fallback_when_library_missing(tmp_path, monkeypatch):
