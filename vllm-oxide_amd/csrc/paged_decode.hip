@@ -603,7 +603,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_persistent(DecodePar
 // another, no cross-wave merge: a sequence wholly inside the range writes its
 // output from registers; a piece writes a partial to slot (u, kh, 0) (the
 // range's first sequence) or (u, kh, 1) (its last), and pass 2
-// (paged_decode_merge_persistent<.., true>) combines the pieces.
+// (paged_decode_merge_stream) combines the pieces.
 constexpr int kStreamWaves = 8;
 
 // Per-wave epilogue of a segment: query slot s < G of lane group 0 holds
@@ -836,13 +836,10 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge(DecodeParams p) {
   }
 }
 
-// Pass 2 of the balanced paths: per (query head, sequence), the pieces of its
-// (b, kh) from range owners owner(g0) .. owner(g0 + L - 1), combined with
-// log-sum-exp weights (a piece outside the window has weight 0).  Persistent:
-// owners are workgroups over positions g = Hkv cu[b] + kh L_b + j, rows
-// (w * 2 + slot) * G + q.  Stream: owners are per-head key ranges over
-// g = cu[b] + j, rows ((u * Hkv + kh) * 2 + slot) * G + q.
-template <class Tag, int D, bool STREAM = false>
+// Pass 2 of the persistent path: per (query head, sequence), the pieces of
+// its (b, kh) from workgroups owner(g0) .. owner(g0 + L - 1), combined with
+// log-sum-exp weights (a piece outside the window has weight 0).
+template <class Tag, int D>
 __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(DecodeParams p) {
   constexpr int PER = D / 64;
   __shared__ float s_o[kWaves][D];
@@ -875,9 +872,8 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(Decode
     return;
   }
   const int W = p.num_wgs;
-  const int64_t N = STREAM ? static_cast<int64_t>(p.cu_seqlens_k[p.batch])
-                           : static_cast<int64_t>(p.num_kv_heads) * p.cu_seqlens_k[p.batch];
-  const int64_t g0 = STREAM ? cb : static_cast<int64_t>(p.num_kv_heads) * cb + kh * Lraw;
+  const int64_t N = static_cast<int64_t>(p.num_kv_heads) * p.cu_seqlens_k[p.batch];
+  const int64_t g0 = static_cast<int64_t>(p.num_kv_heads) * cb + kh * Lraw;
   if (g0 + Lraw > N) {  // inconsistent cu_seqlens_k: pass 1 did not cover these keys
     for (int i = threadIdx.x; i < D; i += kThreads) out[i] = 0;
     return;
@@ -886,10 +882,7 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(Decode
   const int64_t wb = owner_wg(g0 + Lraw - 1, N, W);
   if (wa == wb) return;  // one workgroup held all of it and wrote the output
   const int s_first = wa * N / W < g0 ? 1 : 0;
-  auto row = [&](int i) -> int64_t {
-    const int64_t owner = STREAM ? (wa + i) * p.num_kv_heads + kh : wa + i;
-    return (owner * 2 + (i == 0 ? s_first : 0)) * G + q;
-  };
+  auto row = [&](int i) -> int64_t { return ((wa + i) * 2 + (i == 0 ? s_first : 0)) * G + q; };
   // With fewer positions than workgroups some own an empty range and wrote
   // nothing: their slots are skipped.
   auto piece_lse = [&](int i) -> float {
@@ -955,6 +948,91 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(Decode
       out[lane + 64 * k] = pack1(Tag{}, acc * inv);
     }
   }
+}
+
+// Pass 2 of the stream path: one wave per (query head, sequence).  The pieces
+// of its (b, kh) come from key ranges owner(cb) .. owner(cb + L - 1); a lane
+// per piece reads its log2-sum-exp, the weights are reduced across the wave,
+// and each lane then accumulates D / 64 output dims over the pieces, so the
+// whole merge is three dependent rounds of loads (lengths, lse, partials).
+template <class Tag, int D>
+__global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) {
+  constexpr int PER = D / 64;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int G = p.num_heads / p.num_kv_heads;
+  const int kh = h / G;
+  const int q = h % G;
+  const int64_t cb = p.cu_seqlens_k[b];
+  const int64_t Lraw = max(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - cb, int64_t{0});
+  const int64_t N = p.cu_seqlens_k[p.batch];
+  uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + h) * D;
+  if (Lraw == 0 || seq_len(p, b) == 0 || cb + Lraw > N) {
+    // No keys to attend to (or an inconsistent cu_seqlens_k that pass 1 did
+    // not cover): zeros; with the fused append, the first query head of each
+    // kv-head group writes that head's slice of the new row.
+#pragma unroll
+    for (int k = 0; k < PER; ++k) out[lane + 64 * k] = 0;
+    if (p.new_k != nullptr && q == 0 && Lraw == 0) {
+      const int64_t slot = p.slot_mapping[b];
+      if (slot >= 0) {
+        const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
+        const int64_t src = (static_cast<int64_t>(b) * p.num_kv_heads + kh) * D;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) {
+          const int i = lane + 64 * k;
+          const_cast<uint16_t*>(static_cast<const uint16_t*>(p.k))[slot * row_stride + kh * D + i] =
+              static_cast<const uint16_t*>(p.new_k)[src + i];
+          const_cast<uint16_t*>(static_cast<const uint16_t*>(p.v))[slot * row_stride + kh * D + i] =
+              static_cast<const uint16_t*>(p.new_v)[src + i];
+        }
+      }
+    }
+    return;
+  }
+  const int U = p.num_wgs;
+  const int64_t wa = owner_wg(cb, N, U);
+  const int64_t wb = owner_wg(cb + Lraw - 1, N, U);
+  if (wa == wb) return;  // one range held all of it and wrote the output
+  const int s_first = wa * N / U < cb ? 1 : 0;
+  const int n = static_cast<int>(wb - wa + 1);
+  auto row = [&](int i) -> int64_t {
+    return (((wa + i) * p.num_kv_heads + kh) * 2 + (i == 0 ? s_first : 0)) * G + q;
+  };
+  // Pieces of empty ranges (fewer keys than ranges) were never written.
+  auto piece_lse = [&](int i) -> float {
+    const int64_t v = wa + i;
+    return v * N / U < (v + 1) * N / U ? p.part_lse[row(i)] : -INFINITY;
+  };
+  float M = -INFINITY;
+  for (int i = lane; i < n; i += 64) M = fmaxf(M, piece_lse(i));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
+  const float msafe = M == -INFINITY ? 0.f : M;
+  float o[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) o[k] = 0.f;
+  float wsum = 0.f;
+  for (int g = 0; g < n; g += 64) {
+    const int cnt = min(64, n - g);
+    const float lse = lane < cnt ? piece_lse(g + lane) : -INFINITY;
+    const float wl = lse != -INFINITY ? __builtin_amdgcn_exp2f(lse - msafe) : 0.f;
+    float ws = wl;
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ws += __shfl_xor(ws, m);
+    wsum += ws;
+    for (int i = 0; i < cnt; ++i) {
+      const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i));
+      if (wi == 0.f) continue;  // empty or fully windowed-out piece
+      const float* po = p.part_o + row(g + i) * D + lane;
+#pragma unroll
+      for (int k = 0; k < PER; ++k) o[k] = fmaf(wi, po[64 * k], o[k]);
+    }
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+#pragma unroll
+  for (int k = 0; k < PER; ++k) out[lane + 64 * k] = pack1(Tag{}, o[k] * inv);
 }
 
 // Zero output for a batch whose max_seqlen_k is 0 (no split workgroups run).
@@ -1131,9 +1209,8 @@ void launch_stream(DecodeParams p, hipStream_t s) {
   p.num_wgs = wgs * (kStreamWaves / p.num_kv_heads);
   hipLaunchKernelGGL((paged_decode_stream<Tag, D, G>), dim3(static_cast<unsigned>(wgs)), dim3(64 * kStreamWaves), 0,
                      s, p);
-  hipLaunchKernelGGL((paged_decode_merge_persistent<Tag, D, true>),
-                     dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(kThreads),
-                     0, s, p);
+  hipLaunchKernelGGL((paged_decode_merge_stream<Tag, D>),
+                     dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(64), 0, s, p);
 }
 
 template <class Tag, int D>
