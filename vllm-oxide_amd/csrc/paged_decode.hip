@@ -1022,12 +1022,23 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ws += __shfl_xor(ws, m);
     wsum += ws;
-    for (int i = 0; i < cnt; ++i) {
-      const float wi = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i));
-      if (wi == 0.f) continue;  // empty or fully windowed-out piece
-      const float* po = p.part_o + row(g + i) * D + lane;
+    // Eight pieces at a time: all their loads issued before the FMAs.  A
+    // piece with weight 0 (an empty range: its row was never written, or one
+    // wholly left of the window) is selected away, not multiplied.
+    for (int i0 = 0; i0 < cnt; i0 += 8) {
+      float wv[8], pv[8][PER];
 #pragma unroll
-      for (int k = 0; k < PER; ++k) o[k] = fmaf(wi, po[64 * k], o[k]);
+      for (int j = 0; j < 8; ++j) {
+        const int i = i0 + j;
+        wv[j] = i < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i)) : 0.f;
+        const float* po = p.part_o + row(g + min(i, cnt - 1)) * D + lane;
+#pragma unroll
+        for (int k = 0; k < PER; ++k) pv[j][k] = po[64 * k];
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+#pragma unroll
+        for (int k = 0; k < PER; ++k) o[k] = wv[j] != 0.f ? fmaf(wv[j], pv[j][k], o[k]) : o[k];
     }
   }
   const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
