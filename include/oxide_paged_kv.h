@@ -162,17 +162,21 @@ size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
                                              int64_t num_kv_heads, int64_t head_dim,
                                              int64_t max_seqlen_k);
 
-/* Tokens per KV split chosen for these arguments (256, 512 or 1024), or 0
- * when the balanced persistent pass is chosen instead: long contexts, where
- * batch * max_seqlen_k * num_kv_heads reaches 16384 positions per resident
- * workgroup (CUs x 2); it then splits the summed (sequence, kv head, key)
- * positions evenly over one workgroup per resident slot. */
+/* Tokens per KV split chosen for these arguments (256, 512 or 1024) when the
+ * split grid is chosen; -1 when the wave-level stream pass is chosen (kv
+ * heads dividing 8 and at least ~1024 keys per stream range: batch *
+ * max_seqlen_k >= 1024 * CUs * 8 / num_kv_heads; it splits each head's keys
+ * evenly over CUs * 8 / num_kv_heads ranges, one per wave); 0 when the
+ * balanced persistent pass is chosen (other kv head counts at long contexts:
+ * batch * max_seqlen_k * num_kv_heads >= 16384 positions per resident
+ * workgroup). */
 int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
                                             int64_t max_seqlen_k);
 
 /* Process-wide override of that choice (no counterpart in the reference; for
  * tuning and tests): 0 = by shape (default), 1 = always the split grid,
- * 2 = always the persistent pass.  Results agree within rounding either way. */
+ * 2 = always the persistent pass, 3 = the stream pass where the kv heads
+ * divide 8 (else the persistent pass).  Results agree within rounding. */
 void oxide_set_decode_path(int path);
 
 /*
