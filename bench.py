@@ -473,6 +473,7 @@ def main() -> int:
                    "total_keys": int(st.context_lens.sum())},
         "step_mode": "separate append + attention" if args.separate else "fused append + attention (one launch)",
         "attn_us": round(attn_us, 2),
+        "attn_us_p10_p50_p90": [round(float(np.percentile(att_ms, q)) * 1e3, 2) for q in (10, 50, 90)],
         "attn_kv_read_gbps": round(st.kv_read_bytes() / (attn_us * 1e-6) / 1e9, 1),
         "attn_gbps": round(attn_gbps, 1),
         "attn_hbm_frac": round(attn_gbps / HBM_PEAK_GBPS, 4),

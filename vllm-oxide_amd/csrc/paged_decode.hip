@@ -605,6 +605,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_persistent(DecodePar
 // range's first sequence) or (u, kh, 1) (its last), and pass 2
 // (paged_decode_merge_stream) combines the pieces.
 constexpr int kStreamWaves = 8;
+constexpr int kStreamCuLds = 4096;
 
 // Per-wave epilogue of a segment: query slot s < G of lane group 0 holds
 // query s; acc[dt][j] of lane l is slot 4 (l / 16) + j, dim 16 dt + l % 16.
@@ -644,6 +645,14 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   typedef SplitShape<D, G, 2> S2;
   static_assert(S16::VL == S2::VL && S16::WAVE_BYTES == S2::WAVE_BYTES, "tile shapes shared by both block sizes");
   __shared__ __align__(16) char smem[kStreamWaves * S16::WAVE_BYTES];
+  // Sequence boundaries in LDS (the host takes this path only for batches of
+  // at most kStreamCuLds): every segment lookup and the binary search for a
+  // range's first sequence costs LDS reads instead of dependent global loads.
+  // (Read through the LDS array itself: a generic pointer would make them
+  // flat loads, whose waits also drain the K/V loads in flight.)
+  __shared__ uint32_t cu[kStreamCuLds + 1];
+  for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) cu[i] = p.cu_seqlens_k[i];
+  __syncthreads();  // the only barrier: before any wave can leave
   const int Hkv = p.num_kv_heads;  // divides 8 (checked on the host)
   const int P = kStreamWaves / Hkv;
   const int U = p.num_wgs;         // key ranges per head: gridDim.x * P
@@ -654,7 +663,7 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int kh = wv % Hkv;
   const int u = wg * P + wv / Hkv;
-  const int64_t K = p.cu_seqlens_k[p.batch];
+  const int64_t K = cu[p.batch];
   const int64_t R0 = static_cast<int64_t>(u) * K / U;
   const int64_t R1 = static_cast<int64_t>(u + 1) * K / U;
   if (R0 >= R1) return;  // no barrier anywhere in this kernel: waves may leave alone
@@ -670,8 +679,8 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   auto seg_at = [&](int64_t x, int bb) -> Seg {
     Seg g{false, 0, 0, 0, 0, 0, 0, false};
     while (x < R1 && bb < p.batch) {
-      const int64_t cb = p.cu_seqlens_k[bb];
-      const int64_t Lraw = max(static_cast<int64_t>(p.cu_seqlens_k[bb + 1]) - cb, int64_t{0});
+      const int64_t cb = cu[bb];
+      const int64_t Lraw = max(static_cast<int64_t>(cu[bb + 1]) - cb, int64_t{0});
       if (x < cb) x = cb;  // only with a decreasing cu_seqlens_k
       if (x >= R1) break;
       if (x >= cb + Lraw) {
@@ -680,7 +689,7 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
       }
       const int j0 = static_cast<int>(x - cb);
       const int j1 = static_cast<int>(min(R1, cb + Lraw) - cb);
-      const int L = seq_len(p, bb);
+      const int L = static_cast<int>(min(Lraw, static_cast<int64_t>(p.max_seqlen_k)));  // seq_len()
       const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
       g = Seg{true, bb, L, j0, j1, max(j0, lo), min(j1, L), j0 == 0 && j1 == Lraw};
       break;
@@ -692,11 +701,11 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   };
 
   uint4 kst[2][S16::VL], vst[2][S16::VL];
-  Seg cur = seg_at(R0, find_seq(p.cu_seqlens_k, p.batch, R0));
+  Seg cur = seg_at(R0, find_seq(cu, p.batch, R0));
   bool first_seg = true;
   bool preloaded = false;
   while (cur.valid) {
-    const Seg nxt = seg_at(p.cu_seqlens_k[cur.b] + static_cast<int64_t>(cur.j1), cur.b);
+    const Seg nxt = seg_at(cu[cur.b] + static_cast<int64_t>(cur.j1), cur.b);
     float m_q = -INFINITY, l_q = 0.f;
     floatx4 acc[S16::NDT];
 #pragma unroll
@@ -1069,8 +1078,11 @@ int device_cu_count();
 // hide their start-up and the XCD-aware order helps more than the balance.
 enum DecodePath { kPathSplit = 1, kPathPersistent = 2, kPathStream = 3 };
 
-// The stream pass needs the kv heads to divide its 8 waves per workgroup.
-bool stream_ok(int64_t num_kv_heads) { return num_kv_heads >= 1 && num_kv_heads <= 8 && 8 % num_kv_heads == 0; }
+// The stream pass needs the kv heads to divide its 8 waves per workgroup and
+// the sequence boundaries to fit its LDS table.
+bool stream_ok(int64_t batch, int64_t num_kv_heads) {
+  return num_kv_heads >= 1 && num_kv_heads <= 8 && 8 % num_kv_heads == 0 && batch <= kStreamCuLds;
+}
 
 // Path by shape (measured on MI355X, K/V read rate against the 8 TB/s peak):
 //   * stream when each of its key ranges holds >= ~1024 keys at the longest
@@ -1084,10 +1096,10 @@ bool stream_ok(int64_t num_kv_heads) { return num_kv_heads >= 1 && num_kv_heads 
 //     shapes, the split grid otherwise.
 DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
   const int forced = g_decode_path.load(std::memory_order_relaxed);
-  if (forced == kPathStream && !stream_ok(num_kv_heads)) return kPathPersistent;
+  if (forced == kPathStream && !stream_ok(batch, num_kv_heads)) return kPathPersistent;
   if (forced >= kPathSplit && forced <= kPathStream) return static_cast<DecodePath>(forced);
   const int64_t cus = device_cu_count();
-  if (stream_ok(num_kv_heads)) {
+  if (stream_ok(batch, num_kv_heads)) {
     const int64_t ranges = cus * (8 / num_kv_heads);
     return batch * max_seqlen_k >= int64_t{1024} * ranges ? kPathStream : kPathSplit;
   }
