@@ -65,6 +65,7 @@ CASES = [
     (2, 28, 4, 128, 16, 300, [2100, 77], 500, "bf16"),                  # G=7 (Qwen2.5-7B), window
     (2, 12, 4, 64, 256, 20, [900, 31], -1, "f16"),                      # G=3, D=64
     (2, 24, 4, 128, 256, 20, [1500, 256], -1, "bf16"),                  # G=6
+    (3, 16, 8, 128, 256, 10, [3, 1, 2], -1, "bf16"),                    # fewer keys than stream ranges
 ]
 
 
@@ -455,3 +456,32 @@ def test_kernels_vs_committed_goldens(device):
                                   int(np.diff(cuk).max()), scale, torch.from_numpy(table).to(device), w)
         torch.cuda.synchronize()
         assert_attn_close(to_f32(out), gold[f"case{i}"])
+
+
+def test_decode_batch_beyond_stream_table(device):
+    """4100 sequences (more than the stream pass's LDS table of sequence boundaries):
+    the stream path, even when forced, falls back to the persistent pass, and every
+    path matches the oracle on sampled sequences."""
+    import torch
+    import oxide_paged_kv as ox
+
+    B, Hq, Hkv, D, BS = 4100, 8, 8, 64, 16
+    rng = np.random.default_rng(41)
+    lens = rng.integers(0, 40, B)
+    q, kc, vc, cu, table, max_len = _case(41, B, Hq, Hkv, D, BS, int(((lens + BS - 1) // BS).sum()) + 4,
+                                         lens, "bf16")
+    assert ox.split_tokens(B, Hkv, max_len) != -1
+    sample = [0, 1, 2, 1000, 2047, 4096, 4097, B - 1]
+    want = oracle.paged_decode_attention(q[sample], kc, vc,
+                                         np.concatenate([[0], np.cumsum(lens[sample])]).astype(np.uint32),
+                                         table[sample], 0.125, -1, "bf16")
+    try:
+        for path in (0, 1, 2, 3):
+            ox.set_decode_path(path)
+            if path == 3:
+                assert ox.split_tokens(B, Hkv, max_len) == 0
+            print(f"batch {B} path {path}", flush=True)
+            got = to_f32(_run(device, q, kc, vc, cu, table, max_len, 0.125, -1, "bf16"))
+            assert_attn_close(got[sample], want)
+    finally:
+        ox.set_decode_path(0)
