@@ -164,8 +164,9 @@ size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
 
 /* Tokens per KV split chosen for these arguments (256, 512 or 1024) when the
  * split grid is chosen; -1 when the wave-level stream pass is chosen (kv
- * heads dividing 8 and at least ~1024 keys per stream range: batch *
- * max_seqlen_k >= 1024 * CUs * 8 / num_kv_heads; it splits each head's keys
+ * heads dividing 8, at least ~1024 keys per stream range -- batch *
+ * max_seqlen_k >= 1024 * CUs * 8 / num_kv_heads -- and at least 16 sequences
+ * or 4096 keys per range; it splits each head's keys
  * evenly over CUs * 8 / num_kv_heads ranges, one per wave); 0 when the
  * balanced persistent pass is chosen (other kv head counts at long contexts:
  * batch * max_seqlen_k * num_kv_heads >= 16384 positions per resident

@@ -276,6 +276,8 @@ def test_decode_path_policy(device):
     assert ox.split_tokens(64, 8, 8192) == -1
     assert ox.split_tokens(128, 8, 5120) == -1
     assert ox.split_tokens(32, 8, 4096) == 256
+    assert ox.split_tokens(8, 8, 32768) == 512        # few long sequences: split grid
+    assert ox.split_tokens(8, 8, 131072) == -1        # ... unless the ranges reach 4096 keys
     assert ox.split_tokens(16, 16, 131072) == 0
     ox.set_decode_path(1)
     assert ox.split_tokens(64, 8, 8192) == 1024

@@ -1091,7 +1091,10 @@ bool stream_ok(int64_t batch, int64_t num_kv_heads) {
 //     Qwen3-32B B=16 ctx 32k-128k 79.9 % (persistent 77.7 %);
 //   * below that the split grid (Qwen3-0.6B B=32 ctx 0.5k-4k: split 64 %,
 //     stream 54 %: ranges of ~300 keys make the merge and the per-sequence
-//     start-up dominate);
+//     start-up dominate), and also for fewer than 16 sequences unless the
+//     ranges reach 4096 keys (Qwen3-8B B=8 ctx 8k-32k: split 62 %, stream
+//     60 %: each sequence in ~30 pieces; B=16 ctx 4k-16k: stream 66 %, split
+//     64 %);
 //   * kv head counts that do not divide 8 take the persistent pass for long
 //     shapes, the split grid otherwise.
 DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
@@ -1100,8 +1103,8 @@ DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k
   if (forced >= kPathSplit && forced <= kPathStream) return static_cast<DecodePath>(forced);
   const int64_t cus = device_cu_count();
   if (stream_ok(batch, num_kv_heads)) {
-    const int64_t ranges = cus * (8 / num_kv_heads);
-    return batch * max_seqlen_k >= int64_t{1024} * ranges ? kPathStream : kPathSplit;
+    const int64_t keys_per_range = batch * max_seqlen_k / (cus * (8 / num_kv_heads));
+    return keys_per_range >= 1024 && (batch >= 16 || keys_per_range >= 4096) ? kPathStream : kPathSplit;
   }
   return batch * max_seqlen_k * num_kv_heads >= int64_t{16384} * 2 * cus ? kPathPersistent : kPathSplit;
 }
