@@ -11,11 +11,24 @@
 // view [num_blocks, BS, Hkv, D].  Accumulation is fp32; the output is rounded
 // to the cache dtype once.
 //
-// Pass 1 (paged_decode_split): one workgroup of 4 waves per (split, kv head,
-// sequence); a split is 256, 512 or 1024 consecutive logical keys
-// (choose_split_tokens), a quarter per wave, walked as 16-key tiles in straight-line code with a register
-// double buffer (tile t+1's loads are in flight while tile t computes; loads
-// past the wave's last key are clamped to a fetched tile and masked).
+// Three interchangeable first passes, chosen by shape (choose_path), share the
+// per-wave tile code below:
+//   * paged_decode_stream (long batches): 8-wave workgroups, one per CU, wave
+//     i on kv head i % Hkv, each streaming an equal range of the batch's keys
+//     of its head with no barrier; the pieces of a sequence that crosses
+//     ranges merge in paged_decode_merge_stream.
+//   * paged_decode_split (short ones): a workgroup per (split, kv head,
+//     sequence), merged by paged_decode_merge.
+//   * paged_decode_persistent (kv head counts that do not divide 8, long
+//     contexts): a workgroup per resident slot over the (sequence, kv head,
+//     key) positions, merged by paged_decode_merge_persistent.
+//
+// Pass 1 of the split grid (paged_decode_split): one workgroup of 4 waves per
+// (split, kv head, sequence); a split is 256, 512 or 1024 consecutive logical
+// keys (choose_split_tokens), a quarter per wave, walked as 16-key tiles in
+// straight-line code with a register double buffer (tile t+1's loads are in
+// flight while tile t computes; loads past the wave's last key are clamped to
+// a fetched tile and masked).
 //   * K and V rows are loaded as whole 256-byte head rows per 16 lanes, four
 //     rows per instruction, with non-temporal hints: the shape that streams at
 //     full HBM rate.  K is transposed through a wave-private LDS tile into the
@@ -34,8 +47,9 @@
 // Pass 2 (paged_decode_merge): 4 waves per (query head, sequence) merge the
 // splits that intersect [lo, L) with log-sum-exp weights and write out.
 //
-// Both passes read K/V exactly once; the split partials add
-// 2 * Hq * (D+1) * 4 bytes per split (under 1% at split_tokens = 1024).
+// Every path reads K/V exactly once; the partials add 2 * Hq * (D+1) * 4 bytes
+// per split or piece (under 1 % at split_tokens = 1024; 1.8 % of the bytes on
+// the stream path at Qwen3-8B B=64 ctx 2k-8k).
 #include <math.h>
 
 #include <algorithm>
