@@ -3,9 +3,11 @@ the oracle.
 
 Bar: v rows in the cache are bit-exact (a copy).  q and k follow the reference's
 rounding steps; with the norm the only freedom left is the order of the fp32 sum of
-squares (a tree sum on the GPU, an fp64 sum in the oracle), so elements may differ
-by at most one unit in the last place of the 16-bit format, and at most 2 % of them
-may differ at all.  Without the norm (the qkv-bias models) there is no reduction and
+squares (a tree sum on the GPU, an fp64 sum in the oracle), which may move a normed
+element by one unit in the last place of the 16-bit format before the rotation: the
+rotated outputs may then differ by that unit carried through the rotation (bounded by
+the pair's magnitude, see _assert_rotated), and at most 2 % of them may differ at all.
+Inputs whose sums of squares are exact in any order must agree bit for bit.  Without the norm (the qkv-bias models) there is no reduction and
 the result must be bit-exact.
 """
 import numpy as np
@@ -31,6 +33,29 @@ def _assert_ulp(got, want, max_frac):
     return frac
 
 
+def _ulp16(x, dtype):
+    """Spacing of the 16-bit format at |x| (its subnormal spacing below the normal range)."""
+    mant, emin = (7, -126) if dtype == "bf16" else (10, -14)
+    e = np.floor(np.log2(np.maximum(np.abs(x), 2.0 ** emin)))
+    return np.exp2(e - mant)
+
+
+def _assert_rotated(got, want, dtype, D, max_frac):
+    """Rotated q / k rows.  The sum-of-squares order may move a normed element by one
+    ulp before the rotation, which carries it into y1 = x1 c - x2 s (or y2) as up to
+    one ulp of the pair's magnitude hypot(y1, y2) (the rotation preserves it) per
+    operand -- many ulps of y itself where the two products cancel.  Bar: |got - want|
+    <= 2 ulp(hypot) + ulp(want) everywhere, and at most max_frac of the elements differ."""
+    g = oracle.bits_to_f32(got.reshape(-1, D), dtype).astype(np.float64)
+    w = oracle.bits_to_f32(want.reshape(-1, D), dtype).astype(np.float64)
+    partner = np.concatenate([w[:, D // 2:], w[:, :D // 2]], axis=1)
+    bound = 2 * _ulp16(np.hypot(w, partner), dtype) + _ulp16(w, dtype)
+    err = np.abs(g - w)
+    assert np.all(err <= bound), f"max error / bound {float((err / bound).max()):.2f}"
+    frac = float((got != want).mean())
+    assert frac <= max_frac, f"{frac:.4f} of elements differ"
+
+
 def _case(seed, T, Hq, Hkv, D, dtype, weights, pad=0):
     rng = np.random.default_rng(seed)
     row = (Hq + 2 * Hkv) * D
@@ -53,6 +78,10 @@ CASES = [
     (11, 8, 4, 64, "bf16", True, 0),      # D = 64
     (9, 16, 8, 128, "bf16", False, 0),    # no q/k norm: rope only, bit-exact
     (13, 4, 2, 64, "f16", False, 3),      # row stride not a multiple of 8: element copy of v
+    # Beyond the resident grid (16 workgroups per CU x 256 CUs x 32 or 64 tasks): each
+    # lane walks several tasks with the next one prefetched; T leaves a ragged last round.
+    (4099, 32, 8, 128, "bf16", True, 0),
+    (12007, 16, 4, 64, "f16", True, 3),   # the same through the per-element kernel
 ]
 
 
@@ -65,7 +94,8 @@ def test_prologue_vs_oracle(device, case):
     print(f"prologue case T={T} Hq={Hq} Hkv={Hkv} D={D} {dtype} norm={weights} pad={pad}", flush=True)
     qkv, wq, wk, pos = _case(7, T, Hq, Hkv, D, dtype, weights, pad)
     cs = oracle.rope_cos_sin_cache(8192, D, 1_000_000.0)
-    NB, BS = 6, 16
+    BS = 16
+    NB = max(6, -(-3 * T // (2 * BS)))  # room for every token and some free slots
     rng = np.random.default_rng(1)
     slots = rng.permutation(NB * BS)[:T].astype(np.int64)
     slots[1::5] = -1
@@ -85,9 +115,9 @@ def test_prologue_vs_oracle(device, case):
     torch.cuda.synchronize()
     assert np.array_equal(to_bits(vc_g), vc_want)
     if weights:
-        _assert_ulp(to_bits(q), q_want, 0.02)
-        _assert_ulp(to_bits(k), k_want, 0.02)
-        _assert_ulp(to_bits(kc_g), kc_want, 0.02)
+        _assert_rotated(to_bits(q), q_want, dtype, D, 0.02)
+        _assert_rotated(to_bits(k), k_want, dtype, D, 0.02)
+        _assert_rotated(to_bits(kc_g), kc_want, dtype, D, 0.02)
     else:
         assert np.array_equal(to_bits(q), q_want)
         assert np.array_equal(to_bits(k), k_want)
@@ -163,8 +193,8 @@ def test_prologue_without_append(device):
     q, k = ox.qk_norm_rope_and_cache(t(qkv), 8, 4, t(wq), t(wk), 1e-6, torch.from_numpy(cs).to(device),
                                      torch.from_numpy(pos).to(device), return_k=True)
     torch.cuda.synchronize()
-    _assert_ulp(to_bits(q), q_want, 0.02)
-    _assert_ulp(to_bits(k), k_want, 0.02)
+    _assert_rotated(to_bits(q), q_want, "bf16", 128, 0.02)
+    _assert_rotated(to_bits(k), k_want, "bf16", 128, 0.02)
 
 
 def _exact_sum_case(seed, T, Hq, Hkv, D, dtype, tiny_heads=()):

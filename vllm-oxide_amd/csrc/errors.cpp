@@ -1,7 +1,10 @@
-// Per-host-thread error state behind oxide_last_error().  The reference's entry
+// Per-host-thread error state behind oxide_last_error(), and the cached
+// compute-unit count the launch policies size their grids by.  The reference's entry
 // points return void and drop launch errors (reshape_and_cache.cu:30,
 // copy_blocks.cu:30); this library keeps the void ABI and makes the failure
 // queryable instead.
+#include <atomic>
+
 #include "oxide_common.hpp"
 
 namespace oxide {
@@ -15,6 +18,20 @@ void set_error(int code) {
 void check_launch() {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) set_error(OXIDE_ERR_HIP + static_cast<int>(e));
+}
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
+  std::atomic<int>& n = cache[dev % kMaxDevices];
+  int v = n.load(std::memory_order_relaxed);
+  if (v == 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    n.store(v, std::memory_order_relaxed);
+  }
+  return v;
 }
 
 }  // namespace oxide

@@ -18,6 +18,9 @@ void set_error(int code);
 // Checks the launch just issued; records OXIDE_ERR_HIP + code on failure.
 void check_launch();
 
+// Compute units of the current device (cached per device; 256 when the query fails).
+int device_cu_count();
+
 inline int dtype_size(int dtype) {
   switch (dtype) {
     case OXIDE_DTYPE_F16:

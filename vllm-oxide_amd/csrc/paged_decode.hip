@@ -1082,7 +1082,7 @@ int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 // (paged_decode_persistent); 0 = choose by shape.  Set by oxide_set_decode_path.
 std::atomic<int> g_decode_path{0};
 
-int device_cu_count();
+using oxide::device_cu_count;
 
 // The persistent path pays off when each of its workgroups streams a long
 // range: at most batch * max_seqlen_k * Hkv positions over CUs x 2 workgroups.
@@ -1188,18 +1188,6 @@ bool dispatch_group(const DecodeParams& p, int64_t batch, int group, hipStream_t
 constexpr int kMaxWgsPerCu = 4 * OXIDE_PERSIST_MULT;
 constexpr int kMaxDevices = 64;
 
-int device_cu_count() {
-  static std::atomic<int> cache[kMaxDevices] = {};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) dev = 0;
-  std::atomic<int>& n = cache[dev % kMaxDevices];
-  int v = n.load(std::memory_order_relaxed);
-  if (v == 0) {
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    n.store(v, std::memory_order_relaxed);
-  }
-  return v;
-}
 
 template <class Tag, int D, int G>
 void launch_persistent(DecodeParams p, hipStream_t s) {
