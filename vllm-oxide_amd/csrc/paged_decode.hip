@@ -119,6 +119,7 @@ struct DecodeParams {
   int max_splits;
   int batch;
   int num_wgs;  // persistent path: workgroups sharing the flattened key space
+  int stream_deep;  // stream path: two tiles in flight per wave (see launch_stream)
   float scale_log2;
 };
 
@@ -189,6 +190,27 @@ __device__ __forceinline__ bool decode_work_item(const DecodeParams& p, int& spl
 // reads land on disjoint banks.
 
 // Shared layout constants of pass 1.
+// The block table is not written while a kernel runs.  Read through the
+// constant address space (kScalar), wave-uniform lookups compile to scalar
+// loads, counted apart from the K/V vector loads, and a wave keeps two tiles in
+// flight.  Read as ordinary memory they are vector loads: the lookup for tile
+// t + 1, issued after tile t's loads, completes after them (vector loads
+// complete in issue order), so tile t + 1's loads wait for tile t and a wave
+// keeps one tile in flight -- which the stream pass over long ranges prefers
+// (measured on MI355X; see launch_stream).
+template <bool kScalar>
+struct BtEntry {
+  typedef const int32_t type;
+};
+template <>
+struct BtEntry<true> {
+  typedef __attribute__((address_space(4))) const int32_t type;
+};
+template <bool kScalar>
+__device__ __forceinline__ typename BtEntry<kScalar>::type* block_row(const DecodeParams& p, int b) {
+  return (typename BtEntry<kScalar>::type*)(p.block_table + static_cast<int64_t>(b) * p.max_blocks);
+}
+
 template <int D, int G, int TILES>
 struct SplitShape {
   static constexpr int KK = D / 32;
@@ -224,7 +246,7 @@ struct NextTile {
 
 // K/V rows of tile tt of (b, kh) into registers: lane l loads 16-byte chunk
 // l % CH of rows l / CH + RPL j.
-template <int D, int G, int TILES>
+template <int D, int G, int TILES, bool kScalarBt>
 __device__ __forceinline__ void load_tile_rows(const DecodeParams& p, int b, int kh, int tt,
                                                uint4 (&kr)[SplitShape<D, G, TILES>::VL],
                                                uint4 (&vr)[SplitShape<D, G, TILES>::VL]) {
@@ -234,7 +256,7 @@ __device__ __forceinline__ void load_tile_rows(const DecodeParams& p, int b, int
   const int vrow = lane / S::CH;
   const int BS = p.block_size;
   const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
-  const int32_t* bt = p.block_table + b * p.max_blocks;
+  const auto* bt = block_row<kScalarBt>(p, b);
   const int blk = min(max(bt[tt / BS], 0), p.num_blocks - 1);
   const int64_t row0 = static_cast<int64_t>(blk) * BS + tt % BS;
   const uint16_t* kp = static_cast<const uint16_t*>(p.k) + kh * D + (row0 + vrow) * row_stride + 8 * vch;
@@ -250,7 +272,7 @@ __device__ __forceinline__ void load_tile_rows(const DecodeParams& p, int b, int
 // with nx.valid the last step loads tile nx into buffer 0 for the caller's
 // next call (TILES is even), so a wave streams block after block without
 // waiting on a fresh first load.
-template <class Tag, int D, int G, int TILES>
+template <class Tag, int D, int G, int TILES, bool kScalarBt>
 __device__ __forceinline__ void decode_wave_tiles_buf(const DecodeParams& p, char* smem, int b, int kh, int L,
                                                       int w0, int a, int e, const uint4 (&qb)[D / 32],
                                                       float& m_q, float& l_q, floatx4 (&acc)[D / 16],
@@ -269,7 +291,7 @@ __device__ __forceinline__ void decode_wave_tiles_buf(const DecodeParams& p, cha
   const int64_t row_stride = static_cast<int64_t>(p.num_kv_heads) * D;
   const uint16_t* kbase = static_cast<const uint16_t*>(p.k) + kh * D;
   const uint16_t* vbase = static_cast<const uint16_t*>(p.v) + kh * D;
-  const int32_t* bt = p.block_table + b * p.max_blocks;
+  const auto* bt = block_row<kScalarBt>(p, b);
   uint4* s_k = reinterpret_cast<uint4*>(smem + wave * S::WAVE_BYTES);  // [16][CH], swizzled
   char* s_v = smem + wave * S::WAVE_BYTES + S::KBYTES;                    // [32][VRS]
   {
@@ -303,7 +325,7 @@ __device__ __forceinline__ void decode_wave_tiles_buf(const DecodeParams& p, cha
       if (t + 1 < TILES)
         load_tile(t + 1, kst[(t + 1) & 1], vst[(t + 1) & 1]);
       else if (nx.valid)
-        load_tile_rows<D, G, TILES>(p, nx.b, nx.kh, nx.tt, kst[(t + 1) & 1], vst[(t + 1) & 1]);
+        load_tile_rows<D, G, TILES, kScalarBt>(p, nx.b, nx.kh, nx.tt, kst[(t + 1) & 1], vst[(t + 1) & 1]);
       const uint4(&kr)[VL] = kst[t & 1];
       const uint4(&vr)[VL] = vst[t & 1];
       const int tt = w0 + 16 * t;
@@ -411,7 +433,7 @@ __device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* s
   uint4 kst[2][SplitShape<D, G, TILES>::VL], vst[2][SplitShape<D, G, TILES>::VL];
   const NextTile none{false, 0, 0, 0};
   const int64_t slot_new = p.new_k != nullptr ? p.slot_mapping[b] : -1;
-  decode_wave_tiles_buf<Tag, D, G, TILES>(p, smem, b, kh, L, w0, a, e, qb, m_q, l_q, acc, kst, vst, false, none,
+  decode_wave_tiles_buf<Tag, D, G, TILES, true>(p, smem, b, kh, L, w0, a, e, qb, m_q, l_q, acc, kst, vst, false, none,
                                           slot_new);
 }
 
@@ -653,7 +675,7 @@ __device__ __forceinline__ void decode_wave_epilogue(const DecodeParams& p, int 
   }
 }
 
-template <class Tag, int D, int G>
+template <class Tag, int D, int G, bool kDeep>
 __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(DecodeParams p) {
   typedef SplitShape<D, G, 16> S16;
   typedef SplitShape<D, G, 2> S2;
@@ -739,10 +761,10 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
         const int a = max(cur.a, blk0);
         const int e = min(cur.e, blk0 + 16 * step);
         if (big)
-          decode_wave_tiles_buf<Tag, D, G, 16>(p, smem, cur.b, kh, cur.L, blk0, a, e, qb, m_q, l_q, acc, kst, vst,
+          decode_wave_tiles_buf<Tag, D, G, 16, kDeep>(p, smem, cur.b, kh, cur.L, blk0, a, e, qb, m_q, l_q, acc, kst, vst,
                                                 preloaded, nt, slot_new);
         else
-          decode_wave_tiles_buf<Tag, D, G, 2>(p, smem, cur.b, kh, cur.L, blk0, a, e, qb, m_q, l_q, acc, kst, vst,
+          decode_wave_tiles_buf<Tag, D, G, 2, kDeep>(p, smem, cur.b, kh, cur.L, blk0, a, e, qb, m_q, l_q, acc, kst, vst,
                                                preloaded, nt, slot_new);
         preloaded = nt.valid;
         blk0 += 16 * step;
@@ -1111,13 +1133,18 @@ bool stream_ok(int64_t batch, int64_t num_kv_heads) {
 //     64 %);
 //   * kv head counts that do not divide 8 take the persistent pass for long
 //     shapes, the split grid otherwise.
+// The stream pass's keys per range if every sequence had max_seqlen_k keys.
+int64_t stream_keys_per_range(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
+  return batch * max_seqlen_k / (static_cast<int64_t>(device_cu_count()) * (8 / num_kv_heads));
+}
+
 DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
   const int forced = g_decode_path.load(std::memory_order_relaxed);
   if (forced == kPathStream && !stream_ok(batch, num_kv_heads)) return kPathPersistent;
   if (forced >= kPathSplit && forced <= kPathStream) return static_cast<DecodePath>(forced);
   const int64_t cus = device_cu_count();
   if (stream_ok(batch, num_kv_heads)) {
-    const int64_t keys_per_range = batch * max_seqlen_k / (cus * (8 / num_kv_heads));
+    const int64_t keys_per_range = stream_keys_per_range(batch, num_kv_heads, max_seqlen_k);
     return keys_per_range >= 1024 && (batch >= 16 || keys_per_range >= 4096) ? kPathStream : kPathSplit;
   }
   return batch * max_seqlen_k * num_kv_heads >= int64_t{16384} * 2 * cus ? kPathPersistent : kPathSplit;
@@ -1235,8 +1262,19 @@ void launch_stream(DecodeParams p, hipStream_t s) {
   int wgs = device_cu_count();
   wgs -= wgs % kXcds;  // a whole number of workgroups per XCD
   p.num_wgs = wgs * (kStreamWaves / p.num_kv_heads);
-  hipLaunchKernelGGL((paged_decode_stream<Tag, D, G>), dim3(static_cast<unsigned>(wgs)), dim3(64 * kStreamWaves), 0,
-                     s, p);
+  // Two tiles in flight per wave (kDeep) for ranges shorter than 1536 keys by
+  // the policy's estimate.  Measured on MI355X against one tile in flight:
+  // Qwen3-8B B=64 ctx 0.5k-4k 112 vs 118 us, B=16 ctx 4k-16k 125 vs 130 us
+  // (estimate 1024); B=64 ctx 2k-8k 225 vs 222 us, Qwen3-32B B=16 ctx
+  // 32k-128k 847 vs 832 us, B=64 ctx 2k-8k 245 vs 241 us (estimate 2047 and
+  // more).  The shared-prefix, window-4096 batch of 128 gains (285 vs 303 us)
+  // although its estimate is 4096: its shared blocks hit in L2.
+  if (p.stream_deep)
+    hipLaunchKernelGGL((paged_decode_stream<Tag, D, G, true>), dim3(static_cast<unsigned>(wgs)),
+                       dim3(64 * kStreamWaves), 0, s, p);
+  else
+    hipLaunchKernelGGL((paged_decode_stream<Tag, D, G, false>), dim3(static_cast<unsigned>(wgs)),
+                       dim3(64 * kStreamWaves), 0, s, p);
   hipLaunchKernelGGL((paged_decode_merge_stream<Tag, D>),
                      dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(64), 0, s, p);
 }
@@ -1408,6 +1446,7 @@ void decode_attention_impl(void* out, const void* q, const void* new_k, const vo
   p.window_left = window_left < 0 ? -1 : window_left;
   // 0 selects the persistent path, -1 the stream path.
   p.split_tokens = path == kPathPersistent ? 0 : path == kPathStream ? -1 : static_cast<int>(st);
+  p.stream_deep = path == kPathStream && stream_keys_per_range(batch, num_kv_heads, max_seqlen_k) < 1536;
   p.max_splits = static_cast<int>(max_splits);
   p.batch = static_cast<int>(batch);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
