@@ -147,6 +147,28 @@ def test_copy_blocks_vs_oracle(device, shape, dtype):
     assert np.array_equal(gv.view(tint).cpu().numpy().view(raw), vc)
 
 
+@pytest.mark.parametrize("npairs", [65535, 70001])
+def test_copy_blocks_many_pairs(device, npairs):
+    """Up to 65535 pairs the launch puts a pair's slices along the grid's x and the
+    pairs along y; beyond that (y is limited to 65535) pairs go along x.  Both
+    orders, bit-exact against the oracle (small 128-byte blocks)."""
+    import torch
+
+    rng = np.random.default_rng(npairs)
+    shape = (2 * npairs + 3, 8, 1, 8)
+    kc = rng.integers(0, 2**16, size=shape, dtype=np.uint64).astype(np.uint16)
+    vc = rng.integers(0, 2**16, size=shape, dtype=np.uint64).astype(np.uint16)
+    perm = rng.permutation(shape[0])
+    mapping = np.stack([perm[:npairs], perm[npairs:2 * npairs]], axis=1).astype(np.int64)
+    gk = torch.from_numpy(kc.view(np.int16).copy()).to(device).view(torch.bfloat16)
+    gv = torch.from_numpy(vc.view(np.int16).copy()).to(device).view(torch.bfloat16)
+    _ops().copy_blocks(gk, gv, torch.from_numpy(mapping).to(device))
+    oracle.copy_blocks(kc, vc, mapping)
+    torch.cuda.synchronize()
+    assert np.array_equal(gk.view(torch.int16).cpu().numpy().view(np.uint16), kc)
+    assert np.array_equal(gv.view(torch.int16).cpu().numpy().view(np.uint16), vc)
+
+
 def test_copy_blocks_src_equals_dst_is_identity(device):
     import torch
 

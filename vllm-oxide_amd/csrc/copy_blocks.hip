@@ -11,8 +11,8 @@
 // 512 KiB, so a pair is pure HBM streaming.  Each workgroup owns one pair and
 // a 16 KiB slice of it (256 lanes x 4 x 128-bit vectors) and moves the slice
 // of K and of V, keeping 8 independent 128-bit loads in flight per lane before
-// the stores.  blockIdx.x walks pairs, blockIdx.y walks slices, so a launch
-// has pairs x (block_bytes / 16 KiB) workgroups: 4096 for 128 pairs of 512 KiB,
+// the stores.  blockIdx.x walks the slices of a pair, blockIdx.y the pairs, so
+// a launch has pairs x (block_bytes / 16 KiB) workgroups: 4096 for 128 pairs of 512 KiB,
 // enough to cover all 256 CUs many times over.  The copy is bitwise, so every
 // dtype takes the same path; strides that are not a multiple of 16 bytes fall
 // back to a per-element copy.
@@ -43,12 +43,12 @@ __device__ __forceinline__ PairIds pair_ids(const void* ids, int64_t p) {
   }
 }
 
-template <int kMode>
+template <int kMode, bool kSliceMajor>
 __global__ __launch_bounds__(kThreads) void block_copy_vec16(
     const u32x4* __restrict__ k_src, const u32x4* __restrict__ v_src, u32x4* k_dst,
     u32x4* v_dst, const void* __restrict__ ids, int64_t block_vecs) {
-  const PairIds pr = pair_ids<kMode>(ids, blockIdx.x);
-  const int64_t base = static_cast<int64_t>(blockIdx.y) * kVecsPerGroup + threadIdx.x;
+  const PairIds pr = pair_ids<kMode>(ids, kSliceMajor ? blockIdx.y : blockIdx.x);
+  const int64_t base = static_cast<int64_t>(kSliceMajor ? blockIdx.x : blockIdx.y) * kVecsPerGroup + threadIdx.x;
   const u32x4* ks = k_src + pr.src * block_vecs;
   const u32x4* vs = v_src ? v_src + pr.src * block_vecs : nullptr;
   u32x4* kd = k_dst + pr.dst * block_vecs;
@@ -101,11 +101,23 @@ void launch_block_copy(const void* k_src, const void* v_src, void* k_dst, void* 
                    (!v_src || (oxide::aligned16(v_src) && oxide::aligned16(v_dst)));
   if (vec) {
     const int64_t block_vecs = block_bytes / 16;
-    const dim3 grid(static_cast<unsigned>(num_rows),
-                    static_cast<unsigned>((block_vecs + kVecsPerGroup - 1) / kVecsPerGroup));
-    hipLaunchKernelGGL(block_copy_vec16<kMode>, grid, dim3(kThreads), 0, s,
-                       static_cast<const u32x4*>(k_src), static_cast<const u32x4*>(v_src),
-                       static_cast<u32x4*>(k_dst), static_cast<u32x4*>(v_dst), ids, block_vecs);
+    // Slices of one pair in consecutive workgroups (x), pairs along y (at most
+    // 65535 there; more pairs take pairs along x): the workgroups in flight
+    // stream through a few whole blocks rather than one slice of each of many.
+    // Measured on MI355X, 2048 pairs of 1 MiB K+V with consecutive ids: 746 us
+    // (5.76 TB/s read+write) against 822 us with the pairs along x; with
+    // random ids both ~860 us.
+    const unsigned slices = static_cast<unsigned>((block_vecs + kVecsPerGroup - 1) / kVecsPerGroup);
+    const auto* ks = static_cast<const u32x4*>(k_src);
+    const auto* vs = static_cast<const u32x4*>(v_src);
+    auto* kd = static_cast<u32x4*>(k_dst);
+    auto* vd = static_cast<u32x4*>(v_dst);
+    if (num_rows <= 65535)
+      hipLaunchKernelGGL((block_copy_vec16<kMode, true>), dim3(slices, static_cast<unsigned>(num_rows)),
+                         dim3(kThreads), 0, s, ks, vs, kd, vd, ids, block_vecs);
+    else
+      hipLaunchKernelGGL((block_copy_vec16<kMode, false>), dim3(static_cast<unsigned>(num_rows), slices),
+                         dim3(kThreads), 0, s, ks, vs, kd, vd, ids, block_vecs);
   } else {
     const dim3 grid(static_cast<unsigned>(num_rows),
                     static_cast<unsigned>((block_stride + kThreads - 1) / kThreads));
