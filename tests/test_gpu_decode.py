@@ -95,6 +95,45 @@ def test_decode_vs_oracle(device, case, decode_path):
             assert not got[b].any()
 
 
+def _random_shapes(seed, n):
+    """Seeded random shapes over what the fixed cases combine separately: kv heads
+    1/2/3/4/8, groups 1-8 and 16, D 64/128, page sizes 16/32/256, bf16/f16, ragged
+    lengths with empty and tiny sequences, windows; up to 60k keys per case."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        Hkv = int(rng.choice([1, 2, 3, 4, 8]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 16]))
+        D = int(rng.choice([64, 128]))
+        BS = int(rng.choice([16, 32, 256]))
+        dtype = str(rng.choice(["bf16", "f16"]))
+        B = int(rng.integers(1, 81))
+        lens = rng.integers(0, min(max(1, 60000 // B), 6000) + 1, B)
+        if rng.random() < 0.3:
+            lens[rng.integers(0, B)] = 0
+        if rng.random() < 0.3:
+            lens[:] = rng.integers(1, 40, B)
+        if lens.max() == 0:
+            lens[0] = 5
+        window = -1 if rng.random() < 0.6 else int(rng.integers(0, 3000))
+        out.append((B, G * Hkv, Hkv, D, BS, int(((lens + BS - 1) // BS).sum()) + 3, lens.tolist(), window, dtype))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_shapes(2024, 30), ids=[f"r{i}" for i in range(30)])
+def test_decode_random_shapes_vs_oracle(device, case, decode_path):
+    B, Hq, Hkv, D, BS, NB, lens, window, dtype = case
+    q, kc, vc, cu, table, mx = _case(21, B, Hq, Hkv, D, BS, NB, lens, dtype)
+    scale = 1.0 / math.sqrt(D)
+    print(f"decode random B={B} Hq={Hq} Hkv={Hkv} D={D} BS={BS} max={max(lens)} window={window} {dtype} "
+          f"path={decode_path}", flush=True)
+    got = to_f32(_run(device, q, kc, vc, cu, table, mx, scale, window, dtype))
+    assert_attn_close(got, oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype))
+    for b, L in enumerate(lens):
+        if L == 0:
+            assert not got[b].any()
+
+
 def test_decode_reference_smoke_shape(device):
     """attention/mod.rs:277-323 flash_attn_decode_runs: ctx 32, 4 heads, 4 kv heads,
     D 64, one block of 256 -> shape [1, 4, 64], no NaN (and here also parity)."""
