@@ -96,6 +96,41 @@ def test_prefill_paged_vs_oracle(device, case):
                 assert not got[int(cuq[b]) + i].any()
 
 
+def _random_shapes(seed, n):
+    """Seeded random shapes: 1-3 prompts of up to 300 new tokens behind up to 500
+    cached keys (or fewer keys than queries), kv heads 1/2/4/8, groups 1-8 and 16,
+    D 64/128, page sizes 16/32/64/256 (per-row and per-tile block lookups), windows,
+    bf16/f16; at most ~1e9 multiply-adds per case for the oracle."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        B = int(rng.integers(1, 4))
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 3, 4, 5, 6, 7, 8, 16]))
+        D = int(rng.choice([64, 128]))
+        lq = rng.integers(0, 301, B)
+        pre = rng.integers(0, 501, B) if rng.random() < 0.7 else -rng.integers(0, 50, B)
+        lk = np.maximum(lq + pre, 0)
+        if lq.sum() == 0 or lk.sum() == 0:
+            continue
+        if int((lq * lk).sum()) * G * Hkv * D > 1e9:
+            continue
+        window = -1 if rng.random() < 0.6 else int(rng.integers(0, 600))
+        out.append((lq.tolist(), lk.tolist(), G * Hkv, Hkv, D, int(rng.choice([16, 32, 64, 256])), window,
+                    str(rng.choice(["bf16", "f16"]))))
+    return out
+
+
+@pytest.mark.parametrize("case", _random_shapes(77, 24), ids=[f"r{i}" for i in range(24)])
+def test_prefill_random_shapes_vs_oracle(device, case):
+    lq, lk, Hq, Hkv, D, BS, window, dtype = case
+    q, kc, vc, cuq, cuk, table = _case(31, lq, lk, Hq, Hkv, D, BS, dtype)
+    scale = 1.0 / math.sqrt(D)
+    print(f"prefill random lq={lq} lk={lk} Hq={Hq} Hkv={Hkv} D={D} BS={BS} w={window} {dtype}", flush=True)
+    got = to_f32(_gpu(device, q, kc, vc, cuq, cuk, table, scale, window, dtype))
+    assert_attn_close(got, oracle.prefill_attention(q, kc, vc, cuq, cuk, scale, table, window, dtype))
+
+
 @pytest.mark.parametrize("case", [CASES[1], CASES[4], CASES[7]], ids=["prefix", "window", "d64"])
 def test_prefill_contiguous_equals_paged(device, case):
     """flash_attn_varlen form (contiguous K/V): same kernel, so bit-identical to the paged
