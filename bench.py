@@ -38,7 +38,9 @@ sys.path.insert(0, str(REPO))
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
 # rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE summary of the same workload (calibrated HBM
 # bytes per attention call); the committed summary names the config it covers.
-TRAFFIC_PROFILE = {(3, False): REPO / "profiles" / "paged_decode_cfg3.md",
+TRAFFIC_PROFILE = {(2, False): REPO / "profiles" / "paged_decode_cfg2.md",
+                   (3, False): REPO / "profiles" / "paged_decode_cfg3.md",
+                   (4, False): REPO / "profiles" / "paged_decode_cfg4.md",
                    (5, False): REPO / "profiles" / "paged_decode_cfg5.md"}
 
 
