@@ -57,7 +57,7 @@ def _profile_value(path, key: str):
 PASS1_NAMES = {"split": "split grid", "persistent": "persistent balanced", "stream": "wave-level stream"}
 PASS1_KERNELS = {"split": "paged_decode_split + paged_decode_merge",
                  "persistent": "paged_decode_persistent + paged_decode_merge_persistent",
-                 "stream": "paged_decode_stream + paged_decode_merge_persistent"}
+                 "stream": "paged_decode_stream + paged_decode_merge_stream"}
 
 
 def _pass1(split_tokens: int) -> str:
