@@ -15,8 +15,9 @@
 // per-wave tile code below:
 //   * paged_decode_stream (long batches): 8-wave workgroups, one per CU, wave
 //     i on kv head i % Hkv, each streaming an equal range of the batch's keys
-//     of its head with no barrier; the pieces of a sequence that crosses
-//     ranges merge in paged_decode_merge_stream.
+//     (with a window, of its attended keys) of its head with no barrier; the
+//     pieces of a sequence that crosses ranges merge in
+//     paged_decode_merge_stream.
 //   * paged_decode_split (short ones): a workgroup per (split, kv head,
 //     sequence), merged by paged_decode_merge.
 //   * paged_decode_persistent (kv head counts that do not divide 8, long
@@ -121,6 +122,9 @@ struct DecodeParams {
   int num_wgs;  // persistent path: workgroups sharing the flattened key space
   int stream_deep;  // stream path: two tiles in flight per wave (see launch_stream)
   float scale_log2;
+  // Stream path with a window: prefix sums of the attended keys per sequence
+  // (written by pass 1's first workgroup, read by the merge).
+  uint32_t* attn_cu;
 };
 
 // Keys of sequence b.  Lengths beyond max_seqlen_k (a caller error) are
@@ -675,6 +679,40 @@ __device__ __forceinline__ void decode_wave_epilogue(const DecodeParams& p, int 
   }
 }
 
+// Windowed stream pass: the attended keys of sequence b are [lo_b, L_b) with
+// L_b = seq_len, lo_b = max(0, L_b - 1 - window_left); cu[0..batch] receives
+// their exclusive prefix sums and lo[b] the lo_b (a workgroup scan in LDS:
+// each thread sums a run of sequences, the run totals are scanned, the runs
+// written).  Called by every thread of the workgroup.
+__device__ __forceinline__ void stream_attended_prefix(const DecodeParams& p, uint32_t* cu, int* lo) {
+  constexpr int kT = 64 * kStreamWaves;
+  __shared__ uint32_t run_sum[kT];
+  const int t = threadIdx.x;
+  const int per = (p.batch + kT - 1) / kT;
+  const int b0 = min(p.batch, t * per), b1 = min(p.batch, b0 + per);
+  uint32_t s = 0;
+  for (int b = b0; b < b1; ++b) {
+    const int L = seq_len(p, b);
+    const int l0 = max(0, L - 1 - p.window_left);
+    lo[b] = l0;
+    s += static_cast<uint32_t>(L - l0);
+  }
+  run_sum[t] = s;
+  __syncthreads();
+  for (int off = 1; off < kT; off <<= 1) {  // inclusive scan of the run totals
+    const uint32_t v = t >= off ? run_sum[t - off] : 0u;
+    __syncthreads();
+    run_sum[t] += v;
+    __syncthreads();
+  }
+  uint32_t x = t > 0 ? run_sum[t - 1] : 0u;
+  for (int b = b0; b < b1; ++b) {
+    cu[b] = x;
+    x += static_cast<uint32_t>(seq_len(p, b) - lo[b]);
+  }
+  if (t == kT - 1) cu[p.batch] = run_sum[kT - 1];
+}
+
 template <class Tag, int D, int G, bool kDeep>
 __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(DecodeParams p) {
   typedef SplitShape<D, G, 16> S16;
@@ -687,8 +725,19 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   // (Read through the LDS array itself: a generic pointer would make them
   // flat loads, whose waits also drain the K/V loads in flight.)
   __shared__ uint32_t cu[kStreamCuLds + 1];
-  for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) cu[i] = p.cu_seqlens_k[i];
-  __syncthreads();  // the only barrier: before any wave can leave
+  // With a window the ranges cut the attended keys only -- [lo_b, L_b) of each
+  // sequence, laid end to end, cu holding their prefix sums and win_lo the lo_b
+  // -- so keys before a window start weigh nothing in the balance.
+  __shared__ int win_lo[kStreamCuLds];
+  const bool windowed = p.window_left >= 0;
+  if (!windowed) {
+    for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) cu[i] = p.cu_seqlens_k[i];
+  } else {
+    stream_attended_prefix(p, cu, win_lo);
+    if (blockIdx.x == 0)
+      for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) p.attn_cu[i] = cu[i];
+  }
+  __syncthreads();  // the last barrier: before any wave can leave
   const int Hkv = p.num_kv_heads;  // divides 8 (checked on the host)
   const int P = kStreamWaves / Hkv;
   const int U = p.num_wgs;         // key ranges per head: gridDim.x * P
@@ -712,6 +761,8 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
     int b, L, j0, j1, a, e;
     bool whole;
   };
+  // (With a window, positions are attended keys: offset o of sequence b is
+  // key win_lo[b] + o, and every key of a segment is attended.)
   auto seg_at = [&](int64_t x, int bb) -> Seg {
     Seg g{false, 0, 0, 0, 0, 0, 0, false};
     while (x < R1 && bb < p.batch) {
@@ -723,11 +774,16 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
         ++bb;
         continue;
       }
-      const int j0 = static_cast<int>(x - cb);
-      const int j1 = static_cast<int>(min(R1, cb + Lraw) - cb);
-      const int L = static_cast<int>(min(Lraw, static_cast<int64_t>(p.max_seqlen_k)));  // seq_len()
-      const int lo = p.window_left >= 0 ? max(0, L - 1 - p.window_left) : 0;
-      g = Seg{true, bb, L, j0, j1, max(j0, lo), min(j1, L), j0 == 0 && j1 == Lraw};
+      const int o0 = static_cast<int>(x - cb);
+      const int o1 = static_cast<int>(min(R1, cb + Lraw) - cb);
+      if (windowed) {
+        const int lo = win_lo[bb];
+        const int L = lo + static_cast<int>(Lraw);
+        g = Seg{true, bb, L, lo + o0, lo + o1, lo + o0, lo + o1, o0 == 0 && o1 == Lraw};
+      } else {
+        const int L = static_cast<int>(min(Lraw, static_cast<int64_t>(p.max_seqlen_k)));  // seq_len()
+        g = Seg{true, bb, L, o0, o1, o0, min(o1, L), o0 == 0 && o1 == Lraw};
+      }
       break;
     }
     return g;
@@ -741,7 +797,7 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   bool first_seg = true;
   bool preloaded = false;
   while (cur.valid) {
-    const Seg nxt = seg_at(cu[cur.b] + static_cast<int64_t>(cur.j1), cur.b);
+    const Seg nxt = seg_at(cu[cur.b] + static_cast<int64_t>(cur.j1 - (windowed ? win_lo[cur.b] : 0)), cur.b);
     float m_q = -INFINITY, l_q = 0.f;
     floatx4 acc[S16::NDT];
 #pragma unroll
@@ -1037,10 +1093,15 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
     return;
   }
   const int U = p.num_wgs;
-  const int64_t wa = owner_wg(cb, N, U);
-  const int64_t wb = owner_wg(cb + Lraw - 1, N, U);
+  // Pass 1's key positions: raw keys, or with a window the attended ones
+  // (prefix sums stored by pass 1).
+  const int64_t pb = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[b]) : cb;
+  const int64_t pn = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[b + 1]) - pb : Lraw;
+  const int64_t PN = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[p.batch]) : N;
+  const int64_t wa = owner_wg(pb, PN, U);
+  const int64_t wb = owner_wg(pb + pn - 1, PN, U);
   if (wa == wb) return;  // one range held all of it and wrote the output
-  const int s_first = wa * N / U < cb ? 1 : 0;
+  const int s_first = wa * PN / U < pb ? 1 : 0;
   const int n = static_cast<int>(wb - wa + 1);
   auto row = [&](int i) -> int64_t {
     return (((wa + i) * p.num_kv_heads + kh) * 2 + (i == 0 ? s_first : 0)) * G + q;
@@ -1048,7 +1109,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   // Pieces of empty ranges (fewer keys than ranges) were never written.
   auto piece_lse = [&](int i) -> float {
     const int64_t v = wa + i;
-    return v * N / U < (v + 1) * N / U ? p.part_lse[row(i)] : -INFINITY;
+    return v * PN / U < (v + 1) * PN / U ? p.part_lse[row(i)] : -INFINITY;
   };
   float M = -INFINITY;
   for (int i = lane; i < n; i += 64) M = fmaxf(M, piece_lse(i));
@@ -1267,8 +1328,11 @@ void launch_stream(DecodeParams p, hipStream_t s) {
   // Qwen3-8B B=64 ctx 0.5k-4k 112 vs 118 us, B=16 ctx 4k-16k 125 vs 130 us
   // (estimate 1024); B=64 ctx 2k-8k 225 vs 222 us, Qwen3-32B B=16 ctx
   // 32k-128k 847 vs 832 us, B=64 ctx 2k-8k 245 vs 241 us (estimate 2047 and
-  // more).  The shared-prefix, window-4096 batch of 128 gains (285 vs 303 us)
-  // although its estimate is 4096: its shared blocks hit in L2.
+  // more).  Windowed batches take it too: the shared-prefix, window-4096 batch
+  // of 128 gains (266 vs 285 us; its shared blocks hit in L2) and windowed ones
+  // without sharing measured even (Qwen3-8B B=64 ctx 2k-8k window 4096 170 vs
+  // 171 us, B=128 ctx 4k-5k 349 vs 344 us, Qwen3-32B B=16 ctx 32k-128k window
+  // 8192 110 vs 109 us).
   if (p.stream_deep)
     hipLaunchKernelGGL((paged_decode_stream<Tag, D, G, true>), dim3(static_cast<unsigned>(wgs)),
                        dim3(64 * kStreamWaves), 0, s, p);
@@ -1351,6 +1415,17 @@ int64_t persistent_rows(int64_t num_heads, int64_t num_kv_heads) {
          (num_heads / num_kv_heads);
 }
 
+int64_t partial_rows_max(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t max_seqlen_k) {
+  return std::max(split_rows(batch, num_heads, num_kv_heads, max_seqlen_k), persistent_rows(num_heads, num_kv_heads));
+}
+// The windowed stream pass's attended-key prefix sums follow the partial rows of
+// the largest layout.
+int64_t attn_cu_offset(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                       int64_t max_seqlen_k) {
+  return ceil_div(workspace_layout(partial_rows_max(batch, num_heads, num_kv_heads, max_seqlen_k), head_dim).total,
+                  256) * 256;
+}
+
 }  // namespace
 
 extern "C" int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
@@ -1373,9 +1448,8 @@ extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t n
     return 0;
   // Enough for either path, so a path override between the size query and the
   // call cannot overrun it.
-  const int64_t rows = std::max(split_rows(batch, num_heads, num_kv_heads, max_seqlen_k),
-                                persistent_rows(num_heads, num_kv_heads));
-  return static_cast<size_t>(workspace_layout(rows, head_dim).total);
+  return static_cast<size_t>(attn_cu_offset(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k) +
+                             ceil_div((batch + 1) * 4, 256) * 256);
 }
 
 namespace {
@@ -1446,7 +1520,11 @@ void decode_attention_impl(void* out, const void* q, const void* new_k, const vo
   p.window_left = window_left < 0 ? -1 : window_left;
   // 0 selects the persistent path, -1 the stream path.
   p.split_tokens = path == kPathPersistent ? 0 : path == kPathStream ? -1 : static_cast<int>(st);
-  p.stream_deep = path == kPathStream && stream_keys_per_range(batch, num_kv_heads, max_seqlen_k) < 1536;
+  p.stream_deep = path == kPathStream &&
+                  (stream_keys_per_range(batch, num_kv_heads, max_seqlen_k) < 1536 || window_left >= 0);
+  if (max_seqlen_k > 0)
+    p.attn_cu = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
+                                            attn_cu_offset(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k));
   p.max_splits = static_cast<int>(max_splits);
   p.batch = static_cast<int>(batch);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
