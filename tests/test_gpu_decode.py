@@ -305,6 +305,28 @@ def test_decode_cfg4_prefix_cow_window_full_size(device):
     _check_sampled(st, kc, vc, q, out, [0, 37, 127], c.window_left)
 
 
+def test_decode_windowed_stream_repeats_bit_identical(device):
+    """cfg4 at full size through the windowed stream pass, five calls in a row: the
+    kernels are deterministic, so every call must give the first one's bits (the
+    merge reads the attended-key prefix sums pass 1 publishes; a copy made before
+    every thread had written its part once gave wrong pieces on some calls)."""
+    import torch
+    import oxide_paged_kv as ox
+
+    st, kc, vc, q = _full_size_inputs(4, 43, device)
+    c = st.cfg
+    cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
+    bt = torch.from_numpy(st.block_table).to(device)
+    assert ox.split_tokens(c.batch, c.num_kv_heads, st.max_seqlen_k) == -1
+    outs = [to_bits(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim), c.window_left))
+            for _ in range(5)]
+    for o in outs[1:]:
+        assert np.array_equal(o, outs[0])
+    _check_sampled(st, kc, vc, q, to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k,
+                                                         1 / math.sqrt(c.head_dim), c.window_left)),
+                   [1, 64, 126], c.window_left)
+
+
 def test_decode_path_policy(device):
     """Shapes with >= ~1024 keys per stream range take the wave-level stream pass
     (split_tokens -1: cfg5, cfg3, cfg4), smaller ones a split grid (cfg2); kv head
@@ -330,10 +352,11 @@ def test_decode_path_policy(device):
     ox.set_decode_path(0)
 
 
-@pytest.mark.parametrize("cfg_id", [3, 5])
+@pytest.mark.parametrize("cfg_id", [3, 4, 5])
 def test_decode_paths_agree_full_size(device, cfg_id):
-    """Full-size cfg3 / cfg5 through all three pass-1 paths: outputs agree within
-    rounding of the partial merges (max-abs 2e-2, the attention tolerance)."""
+    """Full-size cfg3 / cfg4 (window 4096: the stream pass balances attended keys) /
+    cfg5 through all three pass-1 paths: outputs agree within rounding of the partial
+    merges (max-abs 2e-2, the attention tolerance)."""
     import torch
     import oxide_paged_kv as ox
 
@@ -346,14 +369,15 @@ def test_decode_paths_agree_full_size(device, cfg_id):
         for path in (1, 2, 3):
             ox.set_decode_path(path)
             print(f"cfg{cfg_id} path {path}", flush=True)
-            outs.append(to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim))))
+            outs.append(to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim),
+                                              None if c.window_left < 0 else c.window_left)))
     finally:
         ox.set_decode_path(0)
     assert_attn_close(outs[1], outs[0])
     assert_attn_close(outs[2], outs[0])
     lens = st.context_lens.astype(np.int64)
     for o in outs[1:]:
-        _check_sampled(st, kc, vc, q, o, [int(lens.argmax()), int(lens.argmin())])
+        _check_sampled(st, kc, vc, q, o, [int(lens.argmax()), int(lens.argmin())], c.window_left)
 
 
 def test_decode_cfg5_long_context_full_size(device):

@@ -734,10 +734,11 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
     for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) cu[i] = p.cu_seqlens_k[i];
   } else {
     stream_attended_prefix(p, cu, win_lo);
-    if (blockIdx.x == 0)
-      for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) p.attn_cu[i] = cu[i];
   }
   __syncthreads();  // the last barrier: before any wave can leave
+  // The merge's copy of the sums (after the barrier: every thread's runs are in).
+  if (windowed && blockIdx.x == 0)
+    for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) p.attn_cu[i] = cu[i];
   const int Hkv = p.num_kv_heads;  // divides 8 (checked on the host)
   const int P = kStreamWaves / Hkv;
   const int U = p.num_wgs;         // key ranges per head: gridDim.x * P
