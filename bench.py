@@ -328,6 +328,8 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--layers", type=int, default=0, help="distinct layers to rotate over (0 = auto)")
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--path", choices=["auto", "split", "persistent", "stream"], default="auto",
+                    help="decode pass 1 (default: the library's choice by shape)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--separate", action="store_true",
                     help="append and attention as two calls (default: one fused call)")
@@ -361,6 +363,7 @@ def main() -> int:
     from oxide_paged_kv.workload import CONFIGS, make_decode_step
 
     cfg = CONFIGS[args.config]
+    ox.set_decode_path({"auto": 0, "split": 1, "persistent": 2, "stream": 3}[args.path])
     dev = torch.device("cuda:0")
     st = make_decode_step(cfg, seed=args.seed)
     layers = args.layers or (cfg.layers if cfg.layers > 1 else 4)
@@ -490,7 +493,7 @@ def main() -> int:
         "tokens_per_s": round(cfg.batch / (ms_per_step * 1e-3), 1),
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": profiled_traffic(args.config, args.separate),
+                     "traffic": profiled_traffic(args.config, args.separate) if args.path == "auto" else None,
                      "kernel": PASS1_KERNELS[_pass1(ox.split_tokens(cfg.batch, H, st.max_seqlen_k))]
                                + " (one attention call" + ("" if args.separate else ", append fused") + ")",
                      "algorithmic_bytes": call_bytes},
