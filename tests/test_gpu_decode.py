@@ -468,9 +468,10 @@ def test_decode_fused_append_equals_append_then_attend(device, case, decode_path
     assert np.array_equal(to_bits(v2), to_bits(v1))
 
 
-@pytest.mark.parametrize("cfg_id", [3, 5])
+@pytest.mark.parametrize("cfg_id", [3, 4, 5])
 def test_decode_fused_append_full_size(device, cfg_id):
-    """Full-size cfg3 / cfg5 step: fused append + attention equals the two calls."""
+    """Full-size cfg3 / cfg4 (window 4096) / cfg5 step: fused append + attention
+    equals the two calls."""
     import torch
     import oxide_paged_kv as ox
 
@@ -485,8 +486,9 @@ def test_decode_fused_append_full_size(device, cfg_id):
     scale = 1 / math.sqrt(c.head_dim)
     k2, v2 = kc.clone(), vc.clone()
     ox.reshape_and_cache(kn, vn, kc, vc, sm)
-    want = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale)
-    got = ox.decode_attn(q, k2, v2, cu, bt, st.max_seqlen_k, scale, append=(kn, vn, sm))
+    w = None if c.window_left < 0 else c.window_left
+    want = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, w)
+    got = ox.decode_attn(q, k2, v2, cu, bt, st.max_seqlen_k, scale, w, append=(kn, vn, sm))
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     assert torch.equal(k2.view(torch.int16), kc.view(torch.int16))
