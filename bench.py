@@ -16,10 +16,13 @@ masks aligned bottom-right) over prompts whose K/V are already in the cache, at
 the Qwen3-8B head shape; its roofline is the matrix cores (bf16 dense peak).
 
 Prints ONE JSON line.  value = algorithmic bytes of (append + attention) per
-step / wall time per step.  The attention call (split-KV kernel + LSE merge
+step / wall time per step.  The attention call (pass-1 kernel + LSE merge
 kernel) is also timed with HIP events on the stream it runs on -> roofline.
-cpu_baseline = the C oracle (test infrastructure, reference semantics) on a
-bounded sample of the same workload.
+The step's K/V/q bytes come from a seeded host generator and are uploaded, so
+cpu_baseline -- the C oracle (test infrastructure, reference semantics) over
+the whole step on the same bytes -- also checks the GPU step's output
+(parity_vs_cpu).  "configs" holds every BASELINE config's fused call measured
+in the same run (device-generated N(0,1) data).
 """
 from __future__ import annotations
 
@@ -72,49 +75,82 @@ def profiled_traffic(config: int, separate: bool):
 PROLOGUE_PROFILE = REPO / "profiles" / "qk_norm_rope_cache_16k.md"
 
 
-def cpu_baseline(cfg, seed: int, threads: int, min_seconds: float = 10.0) -> dict:
-    """Oracle append + attention on the first `n` sequences of the workload."""
+def host_workload(st, seed: int):
+    """The decode step's inputs as host bytes, from the library's seeded generator: K and
+    V of the blocks the batch uses (block ids renumbered 0 .. n-1 in first-use order),
+    q, and the new token's K/V.  The GPU run uploads these exact bytes and the CPU
+    baseline computes on them."""
     import numpy as np
 
-    import oracle
-    from oxide_paged_kv.workload import make_decode_step
+    from oxide_paged_kv.workload import fill_normal
 
-    n = 8
-    st = make_decode_step(cfg, seed=seed, batch=n)
-    rng = np.random.default_rng(seed)
-    rows = st.block_rows
-    used = np.concatenate(rows)
-    nb = len(used)
-    remap = {int(b): i for i, b in enumerate(used)}
+    c = st.cfg
+    used = list(dict.fromkeys([int(x) for r in st.block_rows for x in r] + [int(x) for x in st.cow_pairs[:, 0]]))
+    remap = {b: i for i, b in enumerate(used)}
     table = np.zeros_like(st.block_table)
-    for b, r in enumerate(rows):
+    for b, r in enumerate(st.block_rows):
         table[b, :len(r)] = [remap[int(x)] for x in r]
-    shape = (nb, cfg.block_size, cfg.num_kv_heads, cfg.head_dim)
+    BS = c.block_size
+    slots = np.array([remap[int(s) // BS] * BS + int(s) % BS for s in st.slot_mapping], np.int64)
+    shape = (len(used), BS, c.num_kv_heads, c.head_dim)
+    h = {"used": np.array(used, np.int64), "table": table, "slots": slots,
+         "k": fill_normal(shape, seed, 1), "v": fill_normal(shape, seed, 2),
+         "q": fill_normal((c.batch, c.num_heads, c.head_dim), seed, 3),
+         "knew": fill_normal((c.batch, c.num_kv_heads, c.head_dim), seed, 4),
+         "vnew": fill_normal((c.batch, c.num_kv_heads, c.head_dim), seed, 5)}
+    if len(st.cow_pairs):  # copy-on-write before the append (the GPU side runs copy_blocks)
+        for src, dst in st.cow_pairs:
+            h["k"][remap[int(dst)]] = h["k"][remap[int(src)]]
+            h["v"][remap[int(dst)]] = h["v"][remap[int(src)]]
+    return h
 
-    def bits(shape):
-        return oracle.f32_to_bf16_bits(rng.standard_normal(size=shape, dtype=np.float32)).reshape(shape)
 
-    kc, vc = bits(shape), bits(shape)
-    q = bits((n, cfg.num_heads, cfg.head_dim))
-    knew = bits((n, cfg.num_kv_heads, cfg.head_dim))
-    vnew = bits((n, cfg.num_kv_heads, cfg.head_dim))
-    slots = np.array([table[b, (L - 1) // cfg.block_size] * cfg.block_size + (L - 1) % cfg.block_size
-                      for b, L in enumerate(st.context_lens.astype(np.int64))], dtype=np.int64)
-    scale = 1 / math.sqrt(cfg.head_dim)
+def cpu_baseline(st, h, threads: int, min_seconds: float = 10.0):
+    """The oracle's append + fp32-accumulated attention over the WHOLE step (every
+    sequence of the batch), on the same bytes the GPU run uses; repeated until
+    min_seconds have passed (at least once).  Returns the baseline entry and the
+    output of the last repetition (for the parity check of the bench workload).  The
+    append writes h's K/V in place (the same rows every repetition)."""
+    import oracle
+
+    c = st.cfg
+    k, v = h["k"], h["v"]
+    scale = 1 / math.sqrt(c.head_dim)
     reps, t0 = 0, time.perf_counter()
     while True:
-        oracle.reshape_and_cache(knew, vnew, kc, vc, slots)
-        oracle.paged_decode_attention(q, kc, vc, st.cu_seqlens_k, table, scale, cfg.window_left,
-                                      "bf16", threads=threads)
+        oracle.reshape_and_cache(h["knew"], h["vnew"], k, v, h["slots"])
+        out = oracle.paged_decode_attention(h["q"], k, v, st.cu_seqlens_k, h["table"], scale, c.window_left,
+                                            "bf16", threads=threads)
         reps += 1
         dt = time.perf_counter() - t0
         if dt >= min_seconds:
             break
     step_bytes = st.attn_bytes() + st.append_bytes()
-    return {"value": round(step_bytes * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{n} sequences of the same workload (seed {seed}, {int(st.context_lens.sum())} keys), "
-                      f"append + fp32-accumulated attention, {reps} reps in {dt:.1f} s"}
+    entry = {"value": round(step_bytes * reps / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
+             "host_nproc": os.cpu_count(), "kind": "port",
+             "sample": f"the whole step: all {c.batch} sequences ({int(st.context_lens.sum())} keys), append + "
+                       f"fp32-accumulated attention (C oracle, {threads} threads) on the bytes the GPU run "
+                       f"uploads, {reps} reps in {dt:.1f} s"}
+    return entry, out
+
+
+def parity_vs_cpu(got, want) -> dict:
+    """Bench-workload parity: the GPU step's output against the CPU baseline's, with the
+    target's tolerance (max-abs 2e-2, max-rel 1e-2 floored at 1) and the error bar
+    scaled to each (sequence, head) row (2e-2 max|row| + 1 bf16 ulp)."""
+    import numpy as np
+
+    got = got.astype(np.float64).reshape(-1, got.shape[-1])
+    want = want.astype(np.float64).reshape(-1, want.shape[-1])
+    err = np.abs(got - want)
+    mag = np.abs(want).max(axis=1)
+    ulp = np.exp2(np.floor(np.log2(np.maximum(mag, 2.0 ** -126))) - 7)
+    row_ok = err.max(axis=1) <= 2e-2 * mag + ulp
+    max_abs = float(err.max())
+    max_rel = float((err / np.maximum(np.abs(want), 1.0)).max())
+    return {"max_abs": round(max_abs, 6), "max_rel": round(max_rel, 6),
+            "max_err_over_row_max": round(float((err.max(axis=1) / np.maximum(mag, 1e-30)).max()), 6),
+            "ok": bool(np.isfinite(got).all() and max_abs <= 2e-2 and max_rel <= 1e-2 and row_ok.all())}
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16, published
@@ -331,6 +367,8 @@ def main() -> int:
     ap.add_argument("--path", choices=["auto", "split", "persistent", "stream"], default="auto",
                     help="decode pass 1 (default: the library's choice by shape)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the per-config measurements of the other BASELINE configs")
     ap.add_argument("--separate", action="store_true",
                     help="append and attention as two calls (default: one fused call)")
     ap.add_argument("--prefill", action="store_true",
@@ -356,6 +394,102 @@ def main() -> int:
     if args.prologue:
         return prologue_main(args)
 
+    return decode_main(args)
+
+
+def _device_step_inputs(st, layers: int, dev, seed: int):
+    """Per-config timing inputs generated on the GPU (N(0,1), seeded): the cache buffer
+    [2, layers, NB, BS, Hkv, D] and per-layer q / new K / new V."""
+    import numpy as np
+    import torch
+
+    c = st.cfg
+    g = torch.Generator(device=dev).manual_seed(seed)
+    buf = torch.empty((2, layers, st.pool_blocks, c.block_size, c.num_kv_heads, c.head_dim), dtype=torch.bfloat16,
+                      device=dev)
+    for kv in range(2):
+        for layer in range(layers):
+            buf[kv, layer].normal_(generator=g)
+    q = torch.randn((layers, c.batch, c.num_heads, c.head_dim), generator=g, device=dev).bfloat16()
+    knew = torch.randn((layers, c.batch, c.num_kv_heads, c.head_dim), generator=g, device=dev).bfloat16()
+    vnew = torch.randn((layers, c.batch, c.num_kv_heads, c.head_dim), generator=g, device=dev).bfloat16()
+    meta = (torch.from_numpy(st.slot_mapping).to(dev), torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(dev),
+            torch.from_numpy(st.block_table).to(dev))
+    return buf, q, knew, vnew, meta
+
+
+def measure_config(cfg_id: int, dev, seed: int, steps: int = 20, warmup: int = 5) -> dict:
+    """One BASELINE config's fused append + attention call, averaged over `steps` calls
+    bracketed by two HIP events on the launch stream (no events between calls), the
+    steps rotating over the config's layers (cfg2: its 28 layers; others 4 layers, so no
+    call re-reads what the previous one left in the 256 MB MALL)."""
+    import torch
+
+    import oxide_paged_kv as ox
+    from oxide_paged_kv.workload import CONFIGS, make_decode_step
+
+    cfg = CONFIGS[cfg_id]
+    st = make_decode_step(cfg, seed=seed)
+    layers = cfg.layers if cfg.layers > 1 else 4
+    buf, q, knew, vnew, (sm, cu, bt) = _device_step_inputs(st, layers, dev, seed)
+    out = torch.empty((cfg.batch, cfg.num_heads, cfg.head_dim), dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(max(ox.workspace_size(cfg.batch, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
+                                           st.max_seqlen_k), 1), dtype=torch.uint8, device=dev)
+    scale = 1 / math.sqrt(cfg.head_dim)
+    window = None if cfg.window_left < 0 else cfg.window_left
+    res = {}
+    if len(st.cow_pairs):
+        # Copy-on-write of the shared partial block, once per sequence, before the append.
+        pairs = torch.from_numpy(st.cow_pairs).to(dev)
+        ox.copy_blocks(buf[0, 0], buf[1, 0], pairs)
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        c0.record()
+        for layer in range(layers):
+            ox.copy_blocks(buf[0, layer], buf[1, layer], pairs)
+        c1.record()
+        torch.cuda.synchronize()
+        cow_us = c0.elapsed_time(c1) / layers * 1e3
+        cow_bytes = len(st.cow_pairs) * 2 * 2 * (cfg.block_size * cfg.num_kv_heads * cfg.head_dim * 2) + \
+            16 * len(st.cow_pairs)
+        res["cow_copy_blocks_us"] = round(cow_us, 2)
+        res["cow_copy_blocks_gbps"] = round(cow_bytes / (cow_us * 1e-6) / 1e9, 1)
+
+    def call(i):
+        layer = i % layers
+        ox.decode_attn(q[layer], buf[0, layer], buf[1, layer], cu, bt, st.max_seqlen_k, scale, window,
+                       cfg.block_size, out=out, workspace=ws, append=(knew[layer], vnew[layer], sm))
+
+    for i in range(warmup):
+        call(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        call(warmup + i)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / steps * 1e3
+    nbytes = st.attn_bytes() + st.append_bytes()
+    gbps = nbytes / (us * 1e-6) / 1e9
+    split = ox.split_tokens(cfg.batch, cfg.num_kv_heads, st.max_seqlen_k)
+    traffic = profiled_traffic(cfg_id, False)
+    res.update({"workload": cfg.name, "pass1": PASS1_NAMES[_pass1(split)], "attn_us": round(us, 2),
+                "algorithmic_bytes": nbytes, "attn_gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+                "traffic": traffic, "tokens_per_s": round(cfg.batch / (us * 1e-6), 1),
+                "calls": steps, "layers_rotated": layers})
+    if traffic:
+        # HBM bytes the call actually moves (rocprofv3 FETCH_SIZE + WRITE_SIZE summary
+        # under profiles/) over the same time.
+        res["hbm_frac"] = round(traffic / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)
+    if cfg.layers > 1:
+        res["step_us_all_layers"] = round(us * cfg.layers, 1)
+    del buf
+    torch.cuda.empty_cache()
+    return res
+
+
+def decode_main(args) -> int:
     import numpy as np
     import torch
 
@@ -363,20 +497,27 @@ def main() -> int:
     from oxide_paged_kv.workload import CONFIGS, make_decode_step
 
     cfg = CONFIGS[args.config]
-    ox.set_decode_path({"auto": 0, "split": 1, "persistent": 2, "stream": 3}[args.path])
+    path = ox.DECODE_PATHS[args.path]
     dev = torch.device("cuda:0")
     st = make_decode_step(cfg, seed=args.seed)
     layers = args.layers or (cfg.layers if cfg.layers > 1 else 4)
     NB, BS, H, D = st.pool_blocks, cfg.block_size, cfg.num_kv_heads, cfg.head_dim
-    g = torch.Generator(device=dev).manual_seed(args.seed)
+    # Host bytes of the step (also what the CPU baseline computes on), uploaded into
+    # every rotated layer's blocks: each layer holds the same data at its own address.
+    h = host_workload(st, args.seed)
+    used = torch.from_numpy(h["used"]).to(dev)
+
+    def up(a):
+        return torch.from_numpy(a.view(np.int16)).to(dev).view(torch.bfloat16)
+
     # PagedKVCache buffer [2, L, NB, BS, H, D] (attention/mod.rs:55-85).
-    buf = torch.empty((2, layers, NB, BS, H, D), dtype=torch.bfloat16, device=dev)
-    for kv in range(2):
-        for layer in range(layers):
-            buf[kv, layer].normal_(generator=g)
-    q = torch.randn((layers, cfg.batch, cfg.num_heads, D), generator=g, device=dev).bfloat16()
-    knew = torch.randn((layers, cfg.batch, H, D), generator=g, device=dev).bfloat16()
-    vnew = torch.randn((layers, cfg.batch, H, D), generator=g, device=dev).bfloat16()
+    buf = torch.zeros((2, layers, NB, BS, H, D), dtype=torch.bfloat16, device=dev)
+    kd, vd = up(h["k"]), up(h["v"])
+    for layer in range(layers):
+        buf[0, layer].index_copy_(0, used, kd)
+        buf[1, layer].index_copy_(0, used, vd)
+    del kd, vd
+    q, knew, vnew = up(h["q"]), up(h["knew"]), up(h["vnew"])
     # Metadata uploaded once per step for all layers (not once per layer).
     sm = torch.from_numpy(st.slot_mapping).to(dev)
     cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(dev)
@@ -386,6 +527,10 @@ def main() -> int:
                      dtype=torch.uint8, device=dev)
     scale = 1 / math.sqrt(D)
     window = None if cfg.window_left < 0 else cfg.window_left
+    if len(st.cow_pairs):
+        pairs = torch.from_numpy(st.cow_pairs).to(dev)
+        for layer in range(layers):
+            ox.copy_blocks(buf[0, layer], buf[1, layer], pairs)
 
     def step(i, ev=None):
         layer = i % layers
@@ -393,16 +538,15 @@ def main() -> int:
         if ev:
             ev[0].record()
         if args.separate:
-            ox.reshape_and_cache(knew[layer], vnew[layer], kc, vc, sm)
+            ox.reshape_and_cache(knew, vnew, kc, vc, sm)
             if ev:
                 ev[1].record()
-            ox.decode_attn(q[layer], kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out,
-                           workspace=ws)
+            ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out, workspace=ws, path=path)
         else:
             if ev:
                 ev[1].record()
-            ox.decode_attn(q[layer], kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out,
-                           workspace=ws, append=(knew[layer], vnew[layer], sm))
+            ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out,
+                           workspace=ws, append=(knew, vnew, sm), path=path)
         if ev:
             ev[2].record()
 
@@ -422,6 +566,7 @@ def main() -> int:
     for i in range(args.steps):
         step(args.warmup + i, evs[i])
     torch.cuda.synchronize()
+    gpu_out = out.float().cpu().numpy()  # the last step's output (every layer holds the same inputs)
     att_ms = [e[1].elapsed_time(e[2]) for e in evs]
     ms_per_step = wall * 1e3 / args.steps
     attn_bytes, app_bytes = st.attn_bytes(), st.append_bytes()
@@ -434,17 +579,19 @@ def main() -> int:
     # attention calls are queued first so the GPU is still busy while the host
     # enqueues the short appends: the events then time the device, not the launches.
     for i in range(8):
-        ox.decode_attn(q[i % layers], buf[0, i % layers], buf[1, i % layers], cu, bt, st.max_seqlen_k,
+        ox.decode_attn(q, buf[0, i % layers], buf[1, i % layers], cu, bt, st.max_seqlen_k,
                        scale, window, BS, out=out, workspace=ws)
     a0, a1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a0.record()
     for i in range(20):
         layer = i % layers
-        ox.reshape_and_cache(knew[layer], vnew[layer], buf[0, layer], buf[1, layer], sm)
+        ox.reshape_and_cache(knew, vnew, buf[0, layer], buf[1, layer], sm)
     a1.record()
     torch.cuda.synchronize()
     app_us = a0.elapsed_time(a1) / 20 * 1e3
     app_gbps = app_bytes / (app_us * 1e-6) / 1e9
+    del buf
+    torch.cuda.empty_cache()
 
     extra = {}
     # Achievable-bandwidth calibration: copy_blocks over 1 MiB blocks (read+write).
@@ -462,7 +609,13 @@ def main() -> int:
     cbytes = 2 * nblk * 2 * (BS * H * D * 2)
     extra["stream_copy_gbps"] = round(cbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9, 1)
     del cbuf
+    torch.cuda.empty_cache()
 
+    if not args.no_configs and args.path == "auto" and not args.separate:
+        # Every BASELINE config's fused call, measured in this same run.
+        extra["configs"] = {f"cfg{i}": measure_config(i, dev, args.seed) for i in (1, 2, 3, 4, 5)}
+
+    split = ox.split_tokens(cfg.batch, H, st.max_seqlen_k, path=path)
     res = {
         "metric": "paged-decode attn KV-read GB/s (% HBM peak) + append GB/s, Qwen3-8B shape",
         "value": round(value, 2),
@@ -475,12 +628,12 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic N(0,1) K/V/Q, seeded random block tables",
+        "data": "synthetic N(0,1) K/V/Q from a seeded host generator (the same bytes feed the CPU baseline), "
+                "seeded random block tables",
         "config": {"workload": cfg.name, "batch": cfg.batch, "num_heads": cfg.num_heads,
                    "num_kv_heads": H, "head_dim": D, "block_size": BS, "pool_blocks": NB,
                    "ctx": [cfg.ctx_lo, cfg.ctx_hi], "window_left": cfg.window_left,
-                   "layers_rotated": layers, "split_tokens": ox.split_tokens(cfg.batch, H, st.max_seqlen_k),
-                   "pass1": PASS1_NAMES[_pass1(ox.split_tokens(cfg.batch, H, st.max_seqlen_k))],
+                   "layers_rotated": layers, "split_tokens": split, "pass1": PASS1_NAMES[_pass1(split)],
                    "total_keys": int(st.context_lens.sum())},
         "step_mode": "separate append + attention" if args.separate else "fused append + attention (one launch)",
         "attn_us": round(attn_us, 2),
@@ -494,14 +647,15 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": profiled_traffic(args.config, args.separate) if args.path == "auto" else None,
-                     "kernel": PASS1_KERNELS[_pass1(ox.split_tokens(cfg.batch, H, st.max_seqlen_k))]
+                     "kernel": PASS1_KERNELS[_pass1(split)]
                                + " (one attention call" + ("" if args.separate else ", append fused") + ")",
                      "algorithmic_bytes": call_bytes},
         **extra,
     }
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
-        res["cpu_baseline"] = cpu_baseline(cfg, args.seed, threads)
+        res["cpu_baseline"], cpu_out = cpu_baseline(st, h, threads)
+        res["parity_vs_cpu"] = parity_vs_cpu(gpu_out, cpu_out)
     print(json.dumps(res), flush=True)
     return 0
 

@@ -174,11 +174,31 @@ size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
 int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
                                             int64_t max_seqlen_k);
 
-/* Process-wide override of that choice (no counterpart in the reference; for
- * tuning and tests): 0 = by shape (default), 1 = always the split grid,
- * 2 = always the persistent pass, 3 = the stream pass where the kv heads
- * divide 8 (else the persistent pass).  Results agree within rounding. */
-void oxide_set_decode_path(int path);
+/*
+ * paged_decode_attention (key, value and slot_mapping all NULL) or
+ * paged_decode_attention_append (all three given) with the first pass chosen
+ * by the caller instead of by shape.  No counterpart in the reference; for
+ * tuning and tests.  The choice is an argument of this call only: the library
+ * keeps no state between calls.  path: 0 = by shape (as the plain entries),
+ * 1 = the split grid, 2 = the persistent pass, 3 = the stream pass where the
+ * kv heads divide 8 (else the persistent pass); anything else is
+ * OXIDE_ERR_INVALID_ARGUMENT.  Results agree within rounding; the workspace
+ * size is the same for every path.
+ */
+void paged_decode_attention_path(int path, void* out, const void* q, const void* key, const void* value,
+                                 const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                                 const uint32_t* cu_seqlens_k, const int32_t* block_table,
+                                 int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
+                                 int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                 int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left,
+                                 float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
+                                 void* stream);
+
+/* paged_decode_attention_split_tokens for the first pass that
+ * paged_decode_attention_path(path, ...) runs on these arguments (path 0 =
+ * by shape; codes outside 0..3 read as 0).  No reference counterpart. */
+int64_t paged_decode_attention_path_split_tokens(int path, int64_t batch, int64_t num_kv_heads,
+                                                 int64_t max_seqlen_k);
 
 /*
  * Prefill attention over the paged cache.  Replaces the general (seqlen_q >= 1)

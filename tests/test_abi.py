@@ -79,14 +79,12 @@ def test_workspace_and_split_policy():
     assert ox.split_tokens(1, 1, 100) == 256
     ws = ox.workspace_size(64, 32, 8, 128, 8192)
     assert ws >= 2 * 256 * 8 * 4 * (128 + 1) * 4
-    ox.set_decode_path(1)
-    try:
-        st = ox.split_tokens(64, 8, 8192)
-        assert st % 256 == 0
-        splits = -(-8192 // st)
-        assert ox.workspace_size(64, 32, 8, 128, 8192) >= 64 * 32 * splits * (128 + 1) * 4
-    finally:
-        ox.set_decode_path(0)
+    st = ox.split_tokens(64, 8, 8192, path="split")
+    assert st % 256 == 0
+    splits = -(-8192 // st)
+    assert ox.workspace_size(64, 32, 8, 128, 8192) >= 64 * 32 * splits * (128 + 1) * 4
+    # a forced path is an argument of that call only: the shape policy is unchanged after it
+    assert ox.split_tokens(64, 8, 8192) == -1
     assert ox.workspace_size(64, 32, 8, 128, 0) == 0
 
 

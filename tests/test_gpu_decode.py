@@ -10,12 +10,12 @@ import numpy as np
 import pytest
 
 import oracle
-from helpers import assert_attn_close, normal_bits, to_bits, to_f32, to_torch
+from helpers import assert_attn_close, assert_attn_scaled, normal_bits, to_bits, to_f32, to_torch
 
 pytestmark = pytest.mark.gpu
 
 
-def _run(device, q, kc, vc, cu, table, max_seqlen, scale, window, dtype):
+def _run(device, q, kc, vc, cu, table, max_seqlen, scale, window, dtype, path=0):
     import torch
     import oxide_paged_kv as ox
 
@@ -23,7 +23,7 @@ def _run(device, q, kc, vc, cu, table, max_seqlen, scale, window, dtype):
                          to_torch(vc, dtype, device),
                          torch.from_numpy(cu.view(np.int32)).to(device),
                          torch.from_numpy(np.ascontiguousarray(table, dtype=np.int32)).to(device),
-                         max_seqlen, scale, None if window < 0 else window, kc.shape[1])
+                         max_seqlen, scale, None if window < 0 else window, kc.shape[1], path=path)
     torch.cuda.synchronize()
     return out
 
@@ -73,11 +73,7 @@ CASES = [
 def decode_path(request):
     """Runs a test once per pass-1 path (split grid, persistent balanced pass,
     wave-level stream pass)."""
-    import oxide_paged_kv as ox
-
-    ox.set_decode_path(request.param)
-    yield request.param
-    ox.set_decode_path(0)
+    return request.param
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
@@ -87,7 +83,7 @@ def test_decode_vs_oracle(device, case, decode_path):
     scale = 1.0 / math.sqrt(D)
     print(f"decode case B={B} Hq={Hq} Hkv={Hkv} D={D} BS={BS} lens={lens} window={window} {dtype} "
           f"path={decode_path}", flush=True)
-    got = to_f32(_run(device, q, kc, vc, cu, table, mx, scale, window, dtype))
+    got = to_f32(_run(device, q, kc, vc, cu, table, mx, scale, window, dtype, path=decode_path))
     want = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype)
     assert_attn_close(got, want)
     for b, L in enumerate(lens):
@@ -127,7 +123,7 @@ def test_decode_random_shapes_vs_oracle(device, case, decode_path):
     scale = 1.0 / math.sqrt(D)
     print(f"decode random B={B} Hq={Hq} Hkv={Hkv} D={D} BS={BS} max={max(lens)} window={window} {dtype} "
           f"path={decode_path}", flush=True)
-    got = to_f32(_run(device, q, kc, vc, cu, table, mx, scale, window, dtype))
+    got = to_f32(_run(device, q, kc, vc, cu, table, mx, scale, window, dtype, path=decode_path))
     assert_attn_close(got, oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype))
     for b, L in enumerate(lens):
         if L == 0:
@@ -276,6 +272,7 @@ def _check_sampled(st, kc, vc, q, out, samples, window=-1):
             to_bits(q[b:b + 1]), kb, vb, np.array([0, L], np.uint32),
             np.arange(len(rows), dtype=np.int32)[None], scale, window, threads=16)
         assert_attn_close(out[b:b + 1], want)
+        assert_attn_scaled(out[b:b + 1], want, label=f"seq {b} L={L}")
 
 
 def test_decode_cfg4_prefix_cow_window_full_size(device):
@@ -340,16 +337,12 @@ def test_decode_path_policy(device):
     assert ox.split_tokens(8, 8, 32768) == 512        # few long sequences: split grid
     assert ox.split_tokens(8, 8, 131072) == -1        # ... unless the ranges reach 4096 keys
     assert ox.split_tokens(16, 16, 131072) == 0
-    ox.set_decode_path(1)
-    assert ox.split_tokens(64, 8, 8192) == 1024
-    ox.set_decode_path(0)
-    ox.set_decode_path(1)
-    assert ox.split_tokens(16, 8, 131072) == 1024
-    ox.set_decode_path(2)
-    assert ox.split_tokens(64, 8, 8192) == 0
-    ox.set_decode_path(3)
+    assert ox.split_tokens(64, 8, 8192, path="split") == 1024
+    assert ox.split_tokens(16, 8, 131072, path="split") == 1024
+    assert ox.split_tokens(64, 8, 8192, path="persistent") == 0
+    assert ox.split_tokens(64, 8, 8192, path="stream") == -1
+    assert ox.split_tokens(16, 16, 131072, path="stream") == 0   # kv heads not dividing 8
     assert ox.split_tokens(64, 8, 8192) == -1
-    ox.set_decode_path(0)
 
 
 @pytest.mark.parametrize("cfg_id", [3, 4, 5])
@@ -365,16 +358,14 @@ def test_decode_paths_agree_full_size(device, cfg_id):
     cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
     bt = torch.from_numpy(st.block_table).to(device)
     outs = []
-    try:
-        for path in (1, 2, 3):
-            ox.set_decode_path(path)
-            print(f"cfg{cfg_id} path {path}", flush=True)
-            outs.append(to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim),
-                                              None if c.window_left < 0 else c.window_left)))
-    finally:
-        ox.set_decode_path(0)
+    for path in (1, 2, 3):
+        print(f"cfg{cfg_id} path {path}", flush=True)
+        outs.append(to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim),
+                                          None if c.window_left < 0 else c.window_left, path=path)))
     assert_attn_close(outs[1], outs[0])
     assert_attn_close(outs[2], outs[0])
+    assert_attn_scaled(outs[1], outs[0], label="persistent vs split")
+    assert_attn_scaled(outs[2], outs[0], label="stream vs split")
     lens = st.context_lens.astype(np.int64)
     for o in outs[1:]:
         _check_sampled(st, kc, vc, q, o, [int(lens.argmax()), int(lens.argmin())], c.window_left)
@@ -414,12 +405,8 @@ def test_decode_each_split_size_sampled(device, batch, ctx_hi, want_split):
     q = torch.randn((batch, 32, 128), generator=g, device=device).bfloat16()
     cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
     bt = torch.from_numpy(st.block_table).to(device)
-    ox.set_decode_path(1)
-    try:
-        assert ox.split_tokens(batch, 8, st.max_seqlen_k) == want_split
-        out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(128)))
-    finally:
-        ox.set_decode_path(0)
+    assert ox.split_tokens(batch, 8, st.max_seqlen_k, path="split") == want_split
+    out = to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(128), path="split"))
     lens = st.context_lens.astype(np.int64)
     _check_sampled(st, kc, vc, q, out, sorted({0, int(lens.argmax()), int(lens.argmin()), batch - 1}))
 
@@ -459,9 +446,9 @@ def test_decode_fused_append_equals_append_then_attend(device, case, decode_path
     k1, v1 = to_torch(kc, dtype, device), to_torch(vc, dtype, device)
     kn, vn, sm = to_torch(knew, dtype, device), to_torch(vnew, dtype, device), torch.from_numpy(slots).to(device)
     ox.reshape_and_cache(kn, vn, k1, v1, sm)
-    want = to_bits(ox.decode_attn(*args(k1, v1)))
+    want = to_bits(ox.decode_attn(*args(k1, v1), path=decode_path))
     k2, v2 = to_torch(kc, dtype, device), to_torch(vc, dtype, device)
-    got = to_bits(ox.decode_attn(*args(k2, v2), append=(kn, vn, sm)))
+    got = to_bits(ox.decode_attn(*args(k2, v2), append=(kn, vn, sm), path=decode_path))
     torch.cuda.synchronize()
     assert np.array_equal(got, want)
     assert np.array_equal(to_bits(k2), to_bits(k1))
@@ -542,13 +529,9 @@ def test_decode_batch_beyond_stream_table(device):
     want = oracle.paged_decode_attention(q[sample], kc, vc,
                                          np.concatenate([[0], np.cumsum(lens[sample])]).astype(np.uint32),
                                          table[sample], 0.125, -1, "bf16")
-    try:
-        for path in (0, 1, 2, 3):
-            ox.set_decode_path(path)
-            if path == 3:
-                assert ox.split_tokens(B, Hkv, max_len) == 0
-            print(f"batch {B} path {path}", flush=True)
-            got = to_f32(_run(device, q, kc, vc, cu, table, max_len, 0.125, -1, "bf16"))
-            assert_attn_close(got[sample], want)
-    finally:
-        ox.set_decode_path(0)
+    for path in (0, 1, 2, 3):
+        if path == 3:
+            assert ox.split_tokens(B, Hkv, max_len, path=path) == 0
+        print(f"batch {B} path {path}", flush=True)
+        got = to_f32(_run(device, q, kc, vc, cu, table, max_len, 0.125, -1, "bf16", path=path))
+        assert_attn_close(got[sample], want)

@@ -14,12 +14,14 @@ BIN = REPO / "tests" / "cpp" / "build" / "test_host"
 
 
 def _binary():
-    if not BIN.exists():
-        import importlib.util
+    """The host test binary, rebuilt when it is missing or was built from other sources
+    (build.py keeps a digest of them next to it)."""
+    import importlib.util
 
-        spec = importlib.util.spec_from_file_location("oxide_build", REPO / "vllm-oxide_amd" / "build.py")
-        mod = importlib.util.module_from_spec(spec)
-        spec.loader.exec_module(mod)
+    spec = importlib.util.spec_from_file_location("oxide_build", REPO / "vllm-oxide_amd" / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    if not mod.host_test_current():
         mod.build_host_test()
     return BIN
 
@@ -45,6 +47,6 @@ def test_host_xxh64_matches_python_xxhash():
 
 @pytest.mark.gpu
 def test_host_layer_gpu(device):
-    r = subprocess.run([str(BIN), "gpu"], capture_output=True, text=True, timeout=120)
+    r = subprocess.run([str(_binary()), "gpu"], capture_output=True, text=True, timeout=120)
     assert r.returncode == 0, r.stdout + r.stderr
     assert "gpu: 0 failures" in r.stdout

@@ -23,6 +23,7 @@ BUILD = PKG / "_build"
 LIB = PKG / "liboxide_paged_kv.so"
 HOST_TEST_SRC = REPO / "tests" / "cpp" / "test_host.cpp"
 HOST_TEST_BIN = REPO / "tests" / "cpp" / "build" / "test_host"
+HOST_TEST_STAMP = HOST_TEST_BIN.with_suffix(".sources.sha256")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -66,8 +67,28 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+def host_test_digest() -> str:
+    """Digest of what the host test binary is built from: its source, the host layer,
+    the header and the library it links (content, not mtimes, which a copied tree may
+    not keep)."""
+    import hashlib
+
+    files = [HOST_TEST_SRC, INCLUDE / "oxide_paged_kv.h", LIB, *sorted(HOST.glob("*"))]
+    h = hashlib.sha256()
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes() if f.exists() else b"<missing>")
+    return h.hexdigest()
+
+
+def host_test_current() -> bool:
+    return HOST_TEST_BIN.exists() and HOST_TEST_STAMP.exists() and \
+        HOST_TEST_STAMP.read_text().strip() == host_test_digest()
+
+
 def build_host_test() -> Path:
-    """C++ test binary of the host layer (tests/cpp/test_host.cpp), linked to the library."""
+    """C++ test binary of the host layer (tests/cpp/test_host.cpp), linked to the library;
+    records the digest of its sources next to it."""
     HOST_TEST_BIN.parent.mkdir(parents=True, exist_ok=True)
     cmd = [HIPCC, *HIP_FLAGS, "-I", str(INCLUDE), "-I", str(HOST), "-I", str(PKG / "csrc"), str(HOST_TEST_SRC), "-o",
            str(HOST_TEST_BIN), "-L", str(PKG), "-loxide_paged_kv", f"-Wl,-rpath,{PKG}",
@@ -75,6 +96,7 @@ def build_host_test() -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {HOST_TEST_SRC.name}:\n{r.stdout}\n{r.stderr}")
+    HOST_TEST_STAMP.write_text(host_test_digest())
     return HOST_TEST_BIN
 
 

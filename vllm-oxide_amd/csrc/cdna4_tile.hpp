@@ -90,17 +90,12 @@ __device__ __forceinline__ uint32_t pack2(F16Tag, float lo, float hi) {
   return static_cast<uint32_t>(pack1(F16Tag{}, lo)) | (static_cast<uint32_t>(pack1(F16Tag{}, hi)) << 16);
 }
 
-#ifndef OXIDE_PERMLANE_REDUCE
-#define OXIDE_PERMLANE_REDUCE 1
-#endif
-
 // Reductions over lanes l, l ^ 16, l ^ 32 and l ^ 48: the four 16-lane groups
 // that hold one MFMA column's values.  v_permlane32_swap / v_permlane16_swap
 // exchange lane halves and rows on the VALU (a bpermute shuffle would be an
 // LDS round trip with its wait); the max is a compare-select, which needs no
 // canonicalising moves.  Every lane of the four ends with the same value.
 __device__ __forceinline__ float max_over_lane_groups(float v) {
-#if OXIDE_PERMLANE_REDUCE
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
   v = a > b ? a : b;
@@ -108,10 +103,6 @@ __device__ __forceinline__ float max_over_lane_groups(float v) {
   a = __uint_as_float(s[0]);
   b = __uint_as_float(s[1]);
   return a > b ? a : b;
-#else
-  v = fmaxf(v, __shfl_xor(v, 16));
-  return fmaxf(v, __shfl_xor(v, 32));
-#endif
 }
 
 // Sum over lanes l and l ^ 32 (the two halves of a 32 x 32 MFMA column).
@@ -121,15 +112,10 @@ __device__ __forceinline__ float sum_over_halves(float v) {
 }
 
 __device__ __forceinline__ float sum_over_lane_groups(float v) {
-#if OXIDE_PERMLANE_REDUCE
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   const auto s = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(s[0]) + __uint_as_float(s[1]);
-#else
-  v += __shfl_xor(v, 16);
-  return v + __shfl_xor(v, 32);
-#endif
 }
 
 }  // namespace

@@ -62,36 +62,12 @@
 namespace {
 
 
-// Build-time tuning knobs (defaults are the tuned values).
-#ifndef OXIDE_SPLIT_TOKENS
-#define OXIDE_SPLIT_TOKENS 0  // 0 = policy in choose_split_tokens; else 256, 512 or 1024
-#endif
-#ifndef OXIDE_DECODE_WAVES_PER_EU
-#define OXIDE_DECODE_WAVES_PER_EU 0  // >0: ask the compiler for this occupancy
-#endif
-#if OXIDE_DECODE_WAVES_PER_EU > 0
-#define OXIDE_DECODE_OCCUPANCY __attribute__((amdgpu_waves_per_eu(OXIDE_DECODE_WAVES_PER_EU)))
-#else
-#define OXIDE_DECODE_OCCUPANCY
-#endif
-#ifndef OXIDE_GRID_MODE
-#define OXIDE_GRID_MODE 4  // workgroup -> (split, head, seq) order, see decode_work_item
-#endif
-#ifndef OXIDE_PERSIST_MAP
-#define OXIDE_PERSIST_MAP 1  // persistent range order: 0 = workgroup index, 1 = XCD-major
-#endif
-#ifndef OXIDE_KV_NONTEMPORAL
-#define OXIDE_KV_NONTEMPORAL 1  // 1 = K/V streamed with non-temporal loads
-#endif
-
 // One 16-byte K/V chunk.
+// Non-temporal: K/V are streamed once per call (measured on MI355X: plain
+// loads cost 4-8 % on every decode path).
 __device__ __forceinline__ uint4 load_kv16(const uint16_t* p) {
-#if OXIDE_KV_NONTEMPORAL
   const oxide::u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const oxide::u32x4*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
-#else
-  return *reinterpret_cast<const uint4*>(p);
-#endif
 }
 
 
@@ -140,39 +116,21 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kXcds = 8;  // MI355X: workgroup i runs on XCD i % 8
 
 // Work item (split, kv head, sequence) of this workgroup; false for padding.
-//   mode 0: 3-D grid (split, head, seq), seq slowest.
-//   mode 1: 3-D grid (head, seq, split), split slowest.
-//   mode 2/3: 1-D grid, XCD-grouped: a unit u = (seq, split) is pinned to XCD
-//   u % 8 and its kv heads are consecutive workgroups there, so one XCD reads
-//   all head slices of the unit's token rows together; units are numbered
-//   split-major (2) or seq-major (3).
+// 1-D grid, XCD-grouped: a unit u = (seq, split) is pinned to XCD u % 8 and its
+// kv heads are consecutive workgroups there, so one XCD reads all head slices
+// of the unit's token rows together.  Units are numbered split-major with the
+// sequence rotated by the split index, so consecutive splits of one sequence
+// land on different XCDs and ragged lengths spread evenly over the 8 L2s.
 __device__ __forceinline__ bool decode_work_item(const DecodeParams& p, int& split, int& kh, int& b) {
-#if OXIDE_GRID_MODE == 0
-  split = blockIdx.x; kh = blockIdx.y; b = blockIdx.z;
-  return true;
-#elif OXIDE_GRID_MODE == 1
-  kh = blockIdx.x; b = blockIdx.y; split = blockIdx.z;
-  return true;
-#else
   const int i = blockIdx.x;
   const int j = i / kXcds;
   kh = j % p.num_kv_heads;
   const int u = (j / p.num_kv_heads) * kXcds + i % kXcds;
   const int units = p.batch * p.max_splits;
   if (u >= units) return false;
-#if OXIDE_GRID_MODE == 2
-  b = u % p.batch; split = u / p.batch;
-#elif OXIDE_GRID_MODE == 4
-  // Split-major with the sequence rotated by the split index: unit u sits on
-  // XCD u % 8, so consecutive splits of one sequence land on different XCDs
-  // and ragged lengths spread evenly over the 8 L2s.
   split = u / p.batch;
   b = (u % p.batch + split) % p.batch;
-#else
-  split = u % p.max_splits; b = u / p.max_splits;
-#endif
   return true;
-#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -505,7 +463,7 @@ __device__ __forceinline__ void decode_epilogue(const DecodeParams& p, char* sme
 }
 
 template <class Tag, int D, int G, int TILES>
-__global__ __launch_bounds__(kThreads) OXIDE_DECODE_OCCUPANCY void paged_decode_split(DecodeParams p) {
+__global__ __launch_bounds__(kThreads) void paged_decode_split(DecodeParams p) {
   static_assert(TILES % 2 == 0, "PV steps take two 16-key tiles");
   typedef SplitShape<D, G, TILES> S;
   __shared__ __align__(16) char smem[S::SMEM];
@@ -573,13 +531,9 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_persistent(DecodePar
   typedef SplitShape<D, G, TILES> S;
   __shared__ __align__(16) char smem[S::SMEM];
   const int W = gridDim.x;
-#if OXIDE_PERSIST_MAP == 1
   // Workgroup i runs on XCD i % 8: give each XCD a contiguous eighth of the
   // ranges, so the pieces of one sequence stay in one L2 (W is a multiple of 8).
   const int w = (blockIdx.x % kXcds) * (W / kXcds) + blockIdx.x / kXcds;
-#else
-  const int w = blockIdx.x;
-#endif
   const int Hkv = p.num_kv_heads;
   const int64_t N = static_cast<int64_t>(Hkv) * p.cu_seqlens_k[p.batch];
   const int64_t R0 = static_cast<int64_t>(w) * N / W;
@@ -1162,10 +1116,6 @@ __global__ __launch_bounds__(256) void zero_fill_u16(uint16_t* out, int64_t n) {
 
 int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
-// Pass-1 path: 1 = split grid (paged_decode_split), 2 = persistent balanced
-// (paged_decode_persistent); 0 = choose by shape.  Set by oxide_set_decode_path.
-std::atomic<int> g_decode_path{0};
-
 using oxide::device_cu_count;
 
 // The persistent path pays off when each of its workgroups streams a long
@@ -1200,8 +1150,8 @@ int64_t stream_keys_per_range(int64_t batch, int64_t num_kv_heads, int64_t max_s
   return batch * max_seqlen_k / (static_cast<int64_t>(device_cu_count()) * (8 / num_kv_heads));
 }
 
-DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k) {
-  const int forced = g_decode_path.load(std::memory_order_relaxed);
+// forced: the caller's choice (paged_decode_attention_path), 0 = by shape.
+DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k, int forced) {
   if (forced == kPathStream && !stream_ok(batch, num_kv_heads)) return kPathPersistent;
   if (forced >= kPathSplit && forced <= kPathStream) return static_cast<DecodePath>(forced);
   const int64_t cus = device_cu_count();
@@ -1218,7 +1168,6 @@ int64_t choose_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq
   // so that the ragged tail of the grid stays short.  Measured on MI355X:
   // Qwen3-8B B=64 ctx 2k-8k and Qwen3-32B B=16 ctx 32k-128k are fastest at
   // 1024, Qwen3-0.6B B=32 ctx 0.5k-4k at 256.
-  if (OXIDE_SPLIT_TOKENS > 0) return OXIDE_SPLIT_TOKENS;
   for (int64_t st : {int64_t{1024}, int64_t{512}}) {
     if (batch * num_kv_heads * ceil_div(max_seqlen_k, st) >= 4096) return st;
   }
@@ -1226,14 +1175,8 @@ int64_t choose_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq
 }
 
 dim3 split_grid(const DecodeParams& p) {
-#if OXIDE_GRID_MODE == 0
-  return dim3(p.max_splits, p.num_kv_heads, p.batch);
-#elif OXIDE_GRID_MODE == 1
-  return dim3(p.num_kv_heads, p.batch, p.max_splits);
-#else
   const int64_t units = static_cast<int64_t>(p.batch) * p.max_splits;
   return dim3(static_cast<unsigned>((units + kXcds - 1) / kXcds * kXcds * p.num_kv_heads));
-#endif
 }
 
 template <class Tag, int D, int G, int TILES>
@@ -1271,10 +1214,7 @@ bool dispatch_group(const DecodeParams& p, int64_t batch, int group, hipStream_t
 }
 
 // Workgroups per CU of the persistent path, at most (bounds the workspace).
-#ifndef OXIDE_PERSIST_MULT
-#define OXIDE_PERSIST_MULT 1  // rounds of the balanced pass: workgroups = resident slots x this
-#endif
-constexpr int kMaxWgsPerCu = 4 * OXIDE_PERSIST_MULT;
+constexpr int kMaxWgsPerCu = 4;
 constexpr int kMaxDevices = 64;
 
 
@@ -1293,7 +1233,7 @@ void launch_persistent(DecodeParams p, hipStream_t s) {
     occ = std::max(1, std::min(n, 4));
     occ_cache[dev % kMaxDevices].store(occ, std::memory_order_relaxed);
   }
-  p.num_wgs = device_cu_count() * occ * OXIDE_PERSIST_MULT;
+  p.num_wgs = device_cu_count() * occ;
   p.num_wgs -= p.num_wgs % kXcds;  // a whole number of workgroups per XCD
   hipLaunchKernelGGL((paged_decode_persistent<Tag, D, G>), dim3(static_cast<unsigned>(p.num_wgs)),
                      dim3(kThreads), 0, s, p);
@@ -1429,17 +1369,18 @@ int64_t attn_cu_offset(int64_t batch, int64_t num_heads, int64_t num_kv_heads, i
 
 }  // namespace
 
-extern "C" int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
-                                                       int64_t max_seqlen_k) {
-  switch (choose_path(batch, num_kv_heads, max_seqlen_k)) {
+extern "C" int64_t paged_decode_attention_path_split_tokens(int path, int64_t batch, int64_t num_kv_heads,
+                                                            int64_t max_seqlen_k) {
+  switch (choose_path(batch, num_kv_heads, max_seqlen_k, path >= 0 && path <= 3 ? path : 0)) {
     case kPathPersistent: return 0;
     case kPathStream: return -1;
     default: return choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
   }
 }
 
-extern "C" void oxide_set_decode_path(int path) {
-  g_decode_path.store(path >= 1 && path <= 3 ? path : 0, std::memory_order_relaxed);
+extern "C" int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
+                                                       int64_t max_seqlen_k) {
+  return paged_decode_attention_path_split_tokens(0, batch, num_kv_heads, max_seqlen_k);
 }
 
 extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
@@ -1447,16 +1388,16 @@ extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t n
                                                         int64_t max_seqlen_k) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0)
     return 0;
-  // Enough for either path, so a path override between the size query and the
-  // call cannot overrun it.
+  // Enough for every path, so a forced path (paged_decode_attention_path)
+  // cannot overrun it.
   return static_cast<size_t>(attn_cu_offset(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k) +
                              ceil_div((batch + 1) * 4, 256) * 256);
 }
 
 namespace {
-// Shared body of both entry points; new_k / new_v / slot_mapping are null for
-// plain attention.
-void decode_attention_impl(void* out, const void* q, const void* new_k, const void* new_v,
+// Shared body of the entry points; new_k / new_v / slot_mapping are null for
+// plain attention; forced_path 0 = pass 1 by shape.
+void decode_attention_impl(int forced_path, void* out, const void* q, const void* new_k, const void* new_v,
                            const int64_t* slot_mapping, const void* k_cache, const void* v_cache,
                            const uint32_t* cu_seqlens_k, const int32_t* block_table,
                            int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
@@ -1494,7 +1435,7 @@ void decode_attention_impl(void* out, const void* q, const void* new_k, const vo
     return;
   }
   DecodeParams p{};
-  const DecodePath path = max_seqlen_k > 0 ? choose_path(batch, num_kv_heads, max_seqlen_k) : kPathSplit;
+  const DecodePath path = max_seqlen_k > 0 ? choose_path(batch, num_kv_heads, max_seqlen_k, forced_path) : kPathSplit;
   const bool persistent = path != kPathSplit;
   const int64_t st = max_seqlen_k > 0 ? choose_split_tokens(batch, num_kv_heads, max_seqlen_k) : 1;
   const int64_t max_splits = max_seqlen_k > 0 ? ceil_div(max_seqlen_k, st) : 0;
@@ -1549,19 +1490,20 @@ extern "C" void paged_decode_attention(void* out, const void* q, const void* k_c
                                        int64_t page_block_size, int64_t max_seqlen_k,
                                        int32_t window_left, float softmax_scale, void* workspace,
                                        size_t workspace_bytes, int dtype, void* stream) {
-  decode_attention_impl(out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
+  decode_attention_impl(0, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
                         block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
                         num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
                         softmax_scale, workspace, workspace_bytes, dtype, stream);
 }
 
-extern "C" void paged_decode_attention_append(
-    void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping,
-    void* k_cache, void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table,
-    int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch, int64_t num_heads,
-    int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k,
-    int32_t window_left, float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
-    void* stream) {
+namespace {
+// The fused append + attention with the pass-1 choice given.
+void decode_append_impl(int forced_path, void* out, const void* q, const void* key, const void* value,
+                        const int64_t* slot_mapping, void* k_cache, void* v_cache, const uint32_t* cu_seqlens_k,
+                        const int32_t* block_table, int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
+                        int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
+                        int64_t max_seqlen_k, int32_t window_left, float softmax_scale, void* workspace,
+                        size_t workspace_bytes, int dtype, void* stream) {
   if (batch > 0 && (!key || !value || !slot_mapping || !oxide::aligned16(key) ||
                     !oxide::aligned16(value))) {
     oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
@@ -1571,14 +1513,49 @@ extern "C" void paged_decode_attention_append(
     // No split workgroups run: append through the plain kernel, then zeros.
     reshape_and_cache(key, value, k_cache, v_cache, slot_mapping, batch, num_kv_heads, head_dim,
                       dtype, stream);
-    decode_attention_impl(out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
+    decode_attention_impl(forced_path, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
                           block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
                           num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
                           softmax_scale, workspace, workspace_bytes, dtype, stream);
     return;
   }
-  decode_attention_impl(out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k,
+  decode_attention_impl(forced_path, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k,
                         block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
                         num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
                         softmax_scale, workspace, workspace_bytes, dtype, stream);
+}
+}  // namespace
+
+extern "C" void paged_decode_attention_append(
+    void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping,
+    void* k_cache, void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table,
+    int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch, int64_t num_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k,
+    int32_t window_left, float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
+    void* stream) {
+  decode_append_impl(0, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
+                     max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                     max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" void paged_decode_attention_path(
+    int path, void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping,
+    void* k_cache, void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table,
+    int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch, int64_t num_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k,
+    int32_t window_left, float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
+    void* stream) {
+  if (path < 0 || path > 3) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  if (key == nullptr && value == nullptr && slot_mapping == nullptr) {
+    decode_attention_impl(path, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k, block_table,
+                          max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                          max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream);
+    return;
+  }
+  decode_append_impl(path, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
+                     max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                     max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream);
 }

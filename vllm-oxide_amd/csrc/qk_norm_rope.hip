@@ -95,26 +95,12 @@ constexpr int E = 8;   // elements of each half per lane
 // The qkv rows are read once: non-temporal loads keep them from displacing
 // cached lines.  q, k and v are stored with the default policy (attention reads
 // q next); non-temporal stores measured 3-4 us slower at 16k tokens.
-#ifndef OXIDE_ROPE_NT_LOAD
-#define OXIDE_ROPE_NT_LOAD 1
-#endif
-#ifndef OXIDE_ROPE_NT_STORE
-#define OXIDE_ROPE_NT_STORE 0
-#endif
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ vec_t load_row16(const uint16_t* p) {
-#if OXIDE_ROPE_NT_LOAD
   return __builtin_bit_cast(vec_t, __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p)));
-#else
-  return *reinterpret_cast<const vec_t*>(p);
-#endif
 }
 __device__ __forceinline__ void store_row16(uint16_t* p, vec_t v) {
-#if OXIDE_ROPE_NT_STORE
-  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), reinterpret_cast<u32x4_t*>(p));
-#else
   *reinterpret_cast<vec_t*>(p) = v;
-#endif
 }
 
 // One task's inputs: its token and head, the two 16-byte slices of its qkv
@@ -355,16 +341,15 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_cache_kernel(RopePa
   }
 }
 
-#ifndef OXIDE_ROPE_WGS_PER_CU
-#define OXIDE_ROPE_WGS_PER_CU 16
-#endif
+// Resident workgroups per CU of the prologue grid.
+constexpr int kRopeWgsPerCu = 16;
 template <class Tag>
 bool launch_rope(const RopeParams& p, int64_t num_tokens, int head_dim, hipStream_t s) {
   const int64_t tasks = num_tokens * (p.num_heads + 2 * p.num_kv_heads);
   const int tpw = kRopeThreads / (static_cast<int>(head_dim) / 16);  // tasks per workgroup
   const int64_t wgs = (tasks + tpw - 1) / tpw;
   // A resident grid: each lane walks several tasks, prefetching the next.
-  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(wgs, int64_t{OXIDE_ROPE_WGS_PER_CU} * oxide::device_cu_count())));
+  const dim3 grid(static_cast<unsigned>(std::min<int64_t>(wgs, int64_t{kRopeWgsPerCu} * oxide::device_cu_count())));
   auto kernel = [&](auto d) {
     constexpr int D = decltype(d)::value;
     return p.vec ? qk_norm_rope_cache_kernel<Tag, D, true> : qk_norm_rope_cache_kernel<Tag, D, false>;

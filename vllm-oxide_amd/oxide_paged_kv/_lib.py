@@ -30,7 +30,10 @@ SIGNATURES = {
         ctypes.c_int32, ctypes.c_float, _p, ctypes.c_size_t, ctypes.c_int, _p]),
     "paged_decode_attention_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
     "paged_decode_attention_split_tokens": (_i64, [_i64, _i64, _i64]),
-    "oxide_set_decode_path": (None, [ctypes.c_int]),
+    "paged_decode_attention_path_split_tokens": (_i64, [ctypes.c_int, _i64, _i64, _i64]),
+    "paged_decode_attention_path": (None, [
+        ctypes.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        ctypes.c_int32, ctypes.c_float, _p, ctypes.c_size_t, ctypes.c_int, _p]),
     "paged_prefill_attention": (None, [
         _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
         ctypes.c_int32, ctypes.c_float, ctypes.c_int, _p]),
@@ -42,6 +45,7 @@ SIGNATURES = {
         ctypes.c_int, _p]),
     "oxide_rope_cos_sin_cache": (ctypes.c_int, [_p, _i64, _i64, ctypes.c_float]),
     "build_decode_metadata_device": (None, [_p, _p, _i64, _i64, _i64, _p, _p, _p]),
+    "oxide_fill_normal": (ctypes.c_int, [_p, _i64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_int, ctypes.c_int]),
     "oxide_last_error": (ctypes.c_int, []),
     "oxide_clear_error": (None, []),
     "oxide_error_string": (ctypes.c_char_p, [ctypes.c_int]),

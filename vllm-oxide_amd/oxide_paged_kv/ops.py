@@ -96,23 +96,25 @@ def workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
                                                                  head_dim, max_seqlen_k))
 
 
-def split_tokens(batch: int, num_kv_heads: int, max_seqlen_k: int) -> int:
+def split_tokens(batch: int, num_kv_heads: int, max_seqlen_k: int, path: int | str = 0) -> int:
     """Tokens per KV split of the decode pass 1; 0 for the persistent balanced pass, -1 for
-    the wave-level stream pass."""
-    return int(_lib.load().paged_decode_attention_split_tokens(batch, num_kv_heads, max_seqlen_k))
+    the wave-level stream pass.  path: as for decode_attn (0 / "auto" = by shape)."""
+    L = _lib.load()
+    path = DECODE_PATHS[path] if isinstance(path, str) else int(path)
+    if path == 0:
+        return int(L.paged_decode_attention_split_tokens(batch, num_kv_heads, max_seqlen_k))
+    return int(L.paged_decode_attention_path_split_tokens(path, batch, num_kv_heads, max_seqlen_k))
 
 
-def set_decode_path(path: int) -> None:
-    """0 = choose by shape, 1 = split grid, 2 = persistent balanced pass, 3 = wave-level
-    stream pass (process-wide)."""
-    _lib.load().oxide_set_decode_path(int(path))
+# First-pass names of paged_decode_attention_path.
+DECODE_PATHS = {"auto": 0, "split": 1, "persistent": 2, "stream": 3}
 
 
 def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 cu_seqlens_k: torch.Tensor, block_table: torch.Tensor, max_seqlen_k: int,
                 softmax_scale: float, window_left: int | None = None,
                 page_block_size: int = 256, out: torch.Tensor | None = None,
-                workspace: torch.Tensor | None = None, append=None) -> torch.Tensor:
+                workspace: torch.Tensor | None = None, append=None, path: int | str = 0) -> torch.Tensor:
     """Paged decode attention.
 
     q [B, Hq, D]; k_cache/v_cache [NB, page_block_size, Hkv, D]; cu_seqlens_k uint32-valued
@@ -120,6 +122,8 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     block_table int32 [B, max_blocks] padded with 0; window_left None = unbounded.
     append=(key, value, slot_mapping): first append each sequence's new token (key/value
     [B, Hkv, D], int64 slots) -- fused into the same launch (paged_decode_attention_append).
+    path: the first pass, by name or code of DECODE_PATHS; anything but "auto" / 0 goes
+    through paged_decode_attention_path for this call only.
     """
     L = _lib.load()
     B, Hq, D = q.shape
@@ -141,12 +145,17 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
             -1 if window_left is None else int(window_left), float(softmax_scale),
             _ptr(workspace), workspace.numel() * workspace.element_size(), dtype_code(q.dtype),
             _stream(q))
-    if append is None:
-        L.paged_decode_attention(_ptr(out), _ptr(q), *tail)
-    else:
+    path = DECODE_PATHS[path] if isinstance(path, str) else int(path)
+    if append is not None:
         key, value, slot_mapping = append
         if key.shape != (B, Hkv, D) or value.shape != key.shape or slot_mapping.dtype != torch.int64:
             raise _lib.OxideError("append needs key/value [B, Hkv, D] and int64 slot_mapping [B]")
+    if path != 0:
+        kv = (None, None, None) if append is None else (_ptr(key), _ptr(value), _ptr(slot_mapping))
+        L.paged_decode_attention_path(path, _ptr(out), _ptr(q), *kv, *tail)
+    elif append is None:
+        L.paged_decode_attention(_ptr(out), _ptr(q), *tail)
+    else:
         L.paged_decode_attention_append(_ptr(out), _ptr(q), _ptr(key), _ptr(value),
                                         _ptr(slot_mapping), *tail)
     _lib.check()

@@ -128,3 +128,17 @@ def make_decode_step(cfg: DecodeConfig, seed: int = 0, batch: int | None = None)
     cu = np.zeros(B + 1, dtype=np.uint32)
     cu[1:] = np.cumsum(L).astype(np.uint32)
     return DecodeStep(cfg, L.astype(np.uint32), rows, table, slots, cu, pool, cow)
+
+
+def fill_normal(shape, seed: int, stream: int, dtype: str = "bf16", threads: int = 0) -> np.ndarray:
+    """Seeded N(0, 1) host data from the library's counter-based generator
+    (oxide_fill_normal): uint16 bit patterns for bf16 / f16, float32 for f32.  The same
+    (seed, stream, shape) always gives the same bytes, whatever the thread count."""
+    from . import _lib
+
+    code = {"f16": 0, "bf16": 1, "f32": 2}[dtype]
+    out = np.empty(shape, dtype=np.float32 if code == 2 else np.uint16)
+    rc = _lib.load().oxide_fill_normal(out.ctypes.data, out.size, seed, stream, code, threads)
+    if rc != 0:
+        raise _lib.OxideError(f"oxide_fill_normal: error {rc}")
+    return out
