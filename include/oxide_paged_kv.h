@@ -40,6 +40,7 @@ enum {
   OXIDE_ERR_UNSUPPORTED_DTYPE = 2,
   OXIDE_ERR_UNSUPPORTED_SHAPE = 3, /* head_dim / group size / block size not built */
   OXIDE_ERR_WORKSPACE_TOO_SMALL = 4,
+  OXIDE_ERR_SCRATCH_TOO_SMALL = 5, /* paged_decode_attention_noalloc: shape beyond its static scratch */
   OXIDE_ERR_HIP = 1000 /* OXIDE_ERR_HIP + hipError_t of a failed launch */
 };
 
@@ -303,6 +304,31 @@ int oxide_rope_cos_sin_cache(float* cache, int64_t max_position, int64_t rotary_
 void build_decode_metadata_device(const uint32_t* context_lens, const int32_t* block_table,
                                   int64_t max_blocks_per_seq, int64_t batch, int64_t block_size,
                                   uint32_t* cu_seqlens_k, int64_t* slot_mapping, void* stream);
+
+/*
+ * paged_decode_attention_append (key, value, slot_mapping given) or
+ * paged_decode_attention (all three NULL) without a workspace argument: the
+ * split-KV partials live in a static device array of 48 MiB that each device
+ * holds from the library's load until the process ends.  No counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, serving loops that forbid allocation).  The call allocates
+ * nothing and its kernels need no cleared memory (every partial is written
+ * before it is read).  A shape whose first pass needs more than the array
+ * (its partial rows, their log-sum-exps and, windowed, the attended-key
+ * prefix sums) is rejected with OXIDE_ERR_SCRATCH_TOO_SMALL and launches
+ * nothing; Qwen3 shapes with up to 16 query heads per kv head at head_dim 128
+ * fit at any batch the stream pass takes.  Every call on one device shares
+ * that device's array: calls that overlap in time on one device (two streams,
+ * two threads) race and give wrong results; calls ordered on one stream do not.
+ * Other arguments and results as for paged_decode_attention_append.
+ */
+void paged_decode_attention_noalloc(void* out, const void* q, const void* key, const void* value,
+                                    const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                                    const uint32_t* cu_seqlens_k, const int32_t* block_table,
+                                    int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
+                                    int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                    int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left,
+                                    float softmax_scale, int dtype, void* stream);
 
 /* Error state of the calling host thread: the first error since the last
  * oxide_clear_error(), or OXIDE_OK. */

@@ -1,0 +1,81 @@
+"""paged_decode_attention_noalloc (partials in the library's static device scratch)
+against the workspace entry points, called through the C ABI: bit-identical
+output and caches on two calls in a row, the second with a smaller input (the
+scratch still holds the first call's partials), with and without the fused
+append, windowed and not; a shape beyond the scratch is rejected before any
+launch."""
+import math
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _step(cfg_id, seed, device):
+    import torch
+    from oxide_paged_kv.workload import CONFIGS, make_decode_step
+
+    st = make_decode_step(CONFIGS[cfg_id], seed=seed)
+    c = st.cfg
+    g = torch.Generator(device=device).manual_seed(seed)
+    shape = (st.pool_blocks, c.block_size, c.num_kv_heads, c.head_dim)
+    kc = torch.randn(shape, generator=g, device=device).bfloat16()
+    vc = torch.randn(shape, generator=g, device=device).bfloat16()
+    q = torch.randn((c.batch, c.num_heads, c.head_dim), generator=g, device=device).bfloat16()
+    kn = torch.randn((c.batch, c.num_kv_heads, c.head_dim), generator=g, device=device).bfloat16()
+    vn = torch.randn((c.batch, c.num_kv_heads, c.head_dim), generator=g, device=device).bfloat16()
+    meta = (torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device), torch.from_numpy(st.block_table).to(device))
+    return st, kc, vc, q, (kn, vn, torch.from_numpy(st.slot_mapping).to(device)), meta
+
+
+def _same(a, b):
+    import torch
+
+    return torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("order", [(3, 1), (5, 4)], ids=["cfg3-then-cfg1", "cfg5-then-cfg4"])
+def test_noalloc_matches_workspace_entry(device, order):
+    import torch
+    import oxide_paged_kv as ox
+
+    for cfg_id in order:  # the second call is the smaller input
+        st, kc, vc, q, app, (cu, bt) = _step(cfg_id, 100 + cfg_id, device)
+        c = st.cfg
+        w = None if c.window_left < 0 else c.window_left
+        scale = 1 / math.sqrt(c.head_dim)
+        print(f"noalloc cfg{cfg_id} B={c.batch} window={c.window_left} "
+              f"split_tokens={ox.split_tokens(c.batch, c.num_kv_heads, st.max_seqlen_k)}", flush=True)
+        k2, v2 = kc.clone(), vc.clone()
+        want = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, w, append=app)
+        got = ox.decode_attn(q, k2, v2, cu, bt, st.max_seqlen_k, scale, w, append=app, noalloc=True)
+        torch.cuda.synchronize()
+        assert _same(got, want)
+        assert _same(k2, kc) and _same(v2, vc)
+        want = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, w)
+        got = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, w, noalloc=True)
+        torch.cuda.synchronize()
+        assert _same(got, want)
+        del kc, vc, k2, v2
+        torch.cuda.empty_cache()
+
+
+def test_noalloc_rejects_shape_beyond_scratch(device):
+    """15 sequences of 65536 keys at 128 query heads over 8 kv heads take the split grid
+    with 1024-key splits: 122,880 partial rows of 512 B = 60 MiB > 48 MiB."""
+    import torch
+    import oxide_paged_kv as ox
+    from oxide_paged_kv import _lib
+
+    B, Hq, Hkv, D, L = 15, 128, 8, 128, 65536
+    assert ox.split_tokens(B, Hkv, L) == 1024
+    q = torch.zeros((B, Hq, D), dtype=torch.bfloat16, device=device)
+    kc = torch.zeros((1, 256, Hkv, D), dtype=torch.bfloat16, device=device)
+    out = torch.full_like(q, 7.0)
+    cu = torch.arange(B + 1, dtype=torch.int32, device=device) * L
+    bt = torch.zeros((B, L // 256), dtype=torch.int32, device=device)
+    with pytest.raises(_lib.OxideError, match="error 5"):
+        ox.decode_attn(q, kc, kc, cu, bt, L, 1 / math.sqrt(D), out=out, noalloc=True)
+    torch.cuda.synchronize()
+    assert bool((out.float() == 7.0).all())  # nothing was launched

@@ -52,6 +52,9 @@ extern "C" const char* oxide_error_string(int code) {
       return "unsupported shape (head_dim, group size or block size)";
     case OXIDE_ERR_WORKSPACE_TOO_SMALL:
       return "workspace too small";
+    case OXIDE_ERR_SCRATCH_TOO_SMALL:
+      return "shape needs more partial-result memory than the static scratch of "
+             "paged_decode_attention_noalloc (48 MiB per device)";
     default:
       if (code > OXIDE_ERR_HIP) return hipGetErrorString(static_cast<hipError_t>(code - OXIDE_ERR_HIP));
       return "unknown error";

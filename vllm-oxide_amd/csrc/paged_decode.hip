@@ -55,6 +55,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <mutex>
 
 #include "cdna4_tile.hpp"
 #include "oxide_common.hpp"
@@ -1396,8 +1397,11 @@ extern "C" size_t paged_decode_attention_workspace_size(int64_t batch, int64_t n
 
 namespace {
 // Shared body of the entry points; new_k / new_v / slot_mapping are null for
-// plain attention; forced_path 0 = pass 1 by shape.
-void decode_attention_impl(int forced_path, void* out, const void* q, const void* new_k, const void* new_v,
+// plain attention; forced_path 0 = pass 1 by shape.  With compact_ws the
+// workspace holds only what the chosen first pass touches (its partial rows,
+// then their lse, then the attended-key prefix sums); otherwise it is laid
+// out for every path and must hold paged_decode_attention_workspace_size bytes.
+void decode_attention_impl(bool compact_ws, int forced_path, void* out, const void* q, const void* new_k, const void* new_v,
                            const int64_t* slot_mapping, const void* k_cache, const void* v_cache,
                            const uint32_t* cu_seqlens_k, const int32_t* block_table,
                            int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
@@ -1428,13 +1432,6 @@ void decode_attention_impl(int forced_path, void* out, const void* q, const void
     oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
     return;
   }
-  const size_t need =
-      paged_decode_attention_workspace_size(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k);
-  if (workspace_bytes < need || (need > 0 && !workspace)) {
-    oxide::set_error(OXIDE_ERR_WORKSPACE_TOO_SMALL);
-    return;
-  }
-  DecodeParams p{};
   const DecodePath path = max_seqlen_k > 0 ? choose_path(batch, num_kv_heads, max_seqlen_k, forced_path) : kPathSplit;
   const bool persistent = path != kPathSplit;
   const int64_t st = max_seqlen_k > 0 ? choose_split_tokens(batch, num_kv_heads, max_seqlen_k) : 1;
@@ -1442,6 +1439,18 @@ void decode_attention_impl(int forced_path, void* out, const void* q, const void
   const WorkspaceLayout wl = workspace_layout(
       persistent ? persistent_rows(num_heads, num_kv_heads) : split_rows(batch, num_heads, num_kv_heads, max_seqlen_k),
       head_dim);
+  const int64_t cu_off = max_seqlen_k <= 0 ? 0
+                         : compact_ws ? wl.total
+                                      : attn_cu_offset(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k);
+  const size_t need =
+      max_seqlen_k <= 0 ? 0
+      : compact_ws      ? static_cast<size_t>(cu_off + ceil_div((batch + 1) * 4, 256) * 256)
+                        : paged_decode_attention_workspace_size(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k);
+  if (workspace_bytes < need || (need > 0 && !workspace)) {
+    oxide::set_error(compact_ws ? OXIDE_ERR_SCRATCH_TOO_SMALL : OXIDE_ERR_WORKSPACE_TOO_SMALL);
+    return;
+  }
+  DecodeParams p{};
   p.q = q;
   p.k = k_cache;
   p.v = v_cache;
@@ -1464,9 +1473,7 @@ void decode_attention_impl(int forced_path, void* out, const void* q, const void
   p.split_tokens = path == kPathPersistent ? 0 : path == kPathStream ? -1 : static_cast<int>(st);
   p.stream_deep = path == kPathStream &&
                   (stream_keys_per_range(batch, num_kv_heads, max_seqlen_k) < 1536 || window_left >= 0);
-  if (max_seqlen_k > 0)
-    p.attn_cu = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) +
-                                            attn_cu_offset(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k));
+  if (max_seqlen_k > 0) p.attn_cu = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + cu_off);
   p.max_splits = static_cast<int>(max_splits);
   p.batch = static_cast<int>(batch);
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
@@ -1490,15 +1497,16 @@ extern "C" void paged_decode_attention(void* out, const void* q, const void* k_c
                                        int64_t page_block_size, int64_t max_seqlen_k,
                                        int32_t window_left, float softmax_scale, void* workspace,
                                        size_t workspace_bytes, int dtype, void* stream) {
-  decode_attention_impl(0, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
+  decode_attention_impl(false, 0, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
                         block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
                         num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
                         softmax_scale, workspace, workspace_bytes, dtype, stream);
 }
 
 namespace {
-// The fused append + attention with the pass-1 choice given.
-void decode_append_impl(int forced_path, void* out, const void* q, const void* key, const void* value,
+// The fused append + attention with the pass-1 choice given (compact_ws as for
+// decode_attention_impl).
+void decode_append_impl(bool compact_ws, int forced_path, void* out, const void* q, const void* key, const void* value,
                         const int64_t* slot_mapping, void* k_cache, void* v_cache, const uint32_t* cu_seqlens_k,
                         const int32_t* block_table, int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
                         int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
@@ -1513,13 +1521,13 @@ void decode_append_impl(int forced_path, void* out, const void* q, const void* k
     // No split workgroups run: append through the plain kernel, then zeros.
     reshape_and_cache(key, value, k_cache, v_cache, slot_mapping, batch, num_kv_heads, head_dim,
                       dtype, stream);
-    decode_attention_impl(forced_path, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
+    decode_attention_impl(compact_ws, forced_path, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k,
                           block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
                           num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
                           softmax_scale, workspace, workspace_bytes, dtype, stream);
     return;
   }
-  decode_attention_impl(forced_path, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k,
+  decode_attention_impl(compact_ws, forced_path, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k,
                         block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
                         num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
                         softmax_scale, workspace, workspace_bytes, dtype, stream);
@@ -1533,7 +1541,7 @@ extern "C" void paged_decode_attention_append(
     int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k,
     int32_t window_left, float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
     void* stream) {
-  decode_append_impl(0, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
+  decode_append_impl(false, 0, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
                      max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
                      max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream);
 }
@@ -1550,12 +1558,69 @@ extern "C" void paged_decode_attention_path(
     return;
   }
   if (key == nullptr && value == nullptr && slot_mapping == nullptr) {
-    decode_attention_impl(path, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k, block_table,
+    decode_attention_impl(false, path, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k, block_table,
                           max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
                           max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream);
     return;
   }
-  decode_append_impl(path, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
+  decode_append_impl(false, path, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
                      max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
                      max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream);
+}
+
+// ---------------------------------------------------------------------------
+// The same calls without a caller workspace: the partials live in a static
+// device array, for callers that cannot allocate (code under graph capture,
+// serving loops that forbid allocation).  Each device the library runs on
+// holds its own copy of the array for the life of the process.
+namespace {
+
+constexpr size_t kScratchBytes = size_t{48} << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// `scratch` names a host-side stand-in in host code; the device address of
+// each device's copy comes from hipGetSymbolAddress, taken once per device
+// with that device current, and is the only form host code uses.
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+void* scratch_ptr() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  ScratchSlot& slot = g_scratch[dev];
+  std::call_once(slot.once, [&slot] {
+    void* ptr = nullptr;
+    slot.err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (slot.err == hipSuccess) slot.ptr = ptr;
+  });
+  if (slot.err != hipSuccess) oxide::set_error(OXIDE_ERR_HIP + static_cast<int>(slot.err));
+  return slot.ptr;
+}
+
+}  // namespace
+
+extern "C" void paged_decode_attention_noalloc(
+    void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping,
+    void* k_cache, void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table,
+    int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch, int64_t num_heads,
+    int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k,
+    int32_t window_left, float softmax_scale, int dtype, void* stream) {
+  void* ws = scratch_ptr();
+  if (ws == nullptr) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  if (key == nullptr && value == nullptr && slot_mapping == nullptr) {
+    decode_attention_impl(true, 0, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k, block_table,
+                          max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                          max_seqlen_k, window_left, softmax_scale, ws, kScratchBytes, dtype, stream);
+    return;
+  }
+  decode_append_impl(true, 0, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
+                     max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                     max_seqlen_k, window_left, softmax_scale, ws, kScratchBytes, dtype, stream);
 }

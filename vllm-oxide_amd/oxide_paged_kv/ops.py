@@ -114,7 +114,8 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 cu_seqlens_k: torch.Tensor, block_table: torch.Tensor, max_seqlen_k: int,
                 softmax_scale: float, window_left: int | None = None,
                 page_block_size: int = 256, out: torch.Tensor | None = None,
-                workspace: torch.Tensor | None = None, append=None, path: int | str = 0) -> torch.Tensor:
+                workspace: torch.Tensor | None = None, append=None, path: int | str = 0,
+                noalloc: bool = False) -> torch.Tensor:
     """Paged decode attention.
 
     q [B, Hq, D]; k_cache/v_cache [NB, page_block_size, Hkv, D]; cu_seqlens_k uint32-valued
@@ -124,6 +125,8 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     [B, Hkv, D], int64 slots) -- fused into the same launch (paged_decode_attention_append).
     path: the first pass, by name or code of DECODE_PATHS; anything but "auto" / 0 goes
     through paged_decode_attention_path for this call only.
+    noalloc: call paged_decode_attention_noalloc (partials in the library's static device
+    scratch; no workspace is allocated or passed; path must be "auto").
     """
     L = _lib.load()
     B, Hq, D = q.shape
@@ -136,20 +139,29 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         raise _lib.OxideError("q and caches must share a dtype")
     if out is None:
         out = torch.empty_like(q)
-    need = workspace_size(B, Hq, Hkv, D, max_seqlen_k)
-    if workspace is None or workspace.numel() * workspace.element_size() < need:
-        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
-    max_blocks = block_table.shape[1] if block_table.dim() == 2 else 0
-    tail = (_ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k), _ptr(block_table),
-            max_blocks, NB, B, Hq, Hkv, D, BS, max_seqlen_k,
-            -1 if window_left is None else int(window_left), float(softmax_scale),
-            _ptr(workspace), workspace.numel() * workspace.element_size(), dtype_code(q.dtype),
-            _stream(q))
     path = DECODE_PATHS[path] if isinstance(path, str) else int(path)
     if append is not None:
         key, value, slot_mapping = append
         if key.shape != (B, Hkv, D) or value.shape != key.shape or slot_mapping.dtype != torch.int64:
             raise _lib.OxideError("append needs key/value [B, Hkv, D] and int64 slot_mapping [B]")
+    max_blocks = block_table.shape[1] if block_table.dim() == 2 else 0
+    w = -1 if window_left is None else int(window_left)
+    if noalloc:
+        if path != 0 or workspace is not None:
+            raise _lib.OxideError("noalloc takes no workspace and no forced path")
+        kv = (None, None, None) if append is None else (_ptr(key), _ptr(value), _ptr(slot_mapping))
+        L.paged_decode_attention_noalloc(_ptr(out), _ptr(q), *kv, _ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k),
+                                         _ptr(block_table), max_blocks, NB, B, Hq, Hkv, D, BS, max_seqlen_k, w,
+                                         float(softmax_scale), dtype_code(q.dtype), _stream(q))
+        _lib.check()
+        return out
+    need = workspace_size(B, Hq, Hkv, D, max_seqlen_k)
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+    tail = (_ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k), _ptr(block_table),
+            max_blocks, NB, B, Hq, Hkv, D, BS, max_seqlen_k, w, float(softmax_scale),
+            _ptr(workspace), workspace.numel() * workspace.element_size(), dtype_code(q.dtype),
+            _stream(q))
     if path != 0:
         kv = (None, None, None) if append is None else (_ptr(key), _ptr(value), _ptr(slot_mapping))
         L.paged_decode_attention_path(path, _ptr(out), _ptr(q), *kv, *tail)
