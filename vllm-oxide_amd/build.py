@@ -3,8 +3,10 @@
 The library is built in-tree, next to this file, with plain hipcc calls (no
 cmake, no JIT cache), so the .so travels with the source tree.  Every call
 recompiles.  Counterpart of the reference's crates/vllm-oxide/build.rs:1-30
-(nvcc via cudaforge -> static lib); here hipcc --offload-arch=gfx950 -> shared
-lib that Python loads with ctypes and a Rust crate would link.
+(nvcc via cudaforge -> static lib); here hipcc --offload-arch=gfx950 -> the
+shared library Python loads with ctypes, plus the same objects archived as
+liboxide_paged_kv.a.  rust/oxide-paged-kv-sys/build.rs and
+vllm-oxide_amd/Makefile compile the same sources with the same flags.
 """
 from __future__ import annotations
 
@@ -21,6 +23,7 @@ HOST = PKG / "host"
 INCLUDE = REPO / "include"
 BUILD = PKG / "_build"
 LIB = PKG / "liboxide_paged_kv.so"
+STATIC_LIB = PKG / "liboxide_paged_kv.a"
 HOST_TEST_SRC = REPO / "tests" / "cpp" / "test_host.cpp"
 HOST_TEST_BIN = REPO / "tests" / "cpp" / "build" / "test_host"
 HOST_TEST_STAMP = HOST_TEST_BIN.with_suffix(".sources.sha256")
@@ -61,6 +64,12 @@ def build(verbose: bool = False) -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
+    # The same objects as a static archive (what the Rust crate's build.rs and the
+    # Makefile produce) for hosts that link the kernels statically.
+    STATIC_LIB.unlink(missing_ok=True)
+    r = subprocess.run(["ar", "rcs", str(STATIC_LIB), *map(str, objs)], capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"ar failed:\n{r.stdout}\n{r.stderr}")
     build_host_test()
     if verbose:
         print(f"built {LIB}")
