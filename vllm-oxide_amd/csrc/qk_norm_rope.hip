@@ -131,8 +131,14 @@ __device__ __forceinline__ void split_task(int64_t task, int heads, bool narrow,
   }
 }
 
+// `real` false: a lane with no further task -- the row loads still issue (the
+// waits stay exact) but read the norm weight row (or the cos / sin table),
+// which every task reads with ordinary loads and so sits in L2: re-reading the
+// current task's row would fetch it from HBM again, since the row loads are
+// non-temporal and do not keep their lines.
 template <int D, bool V>
-__device__ __forceinline__ void load_task(const RopeParams& p, int64_t task, int heads, bool narrow, TaskIn& in) {
+__device__ __forceinline__ void load_task(const RopeParams& p, int64_t task, int heads, bool narrow, TaskIn& in,
+                                          bool real = true) {
   constexpr int LPH = kLanesPerHead<D>;
   const int sub = threadIdx.x % LPH;
   split_task(task, heads, narrow, in.t, in.h);
@@ -143,7 +149,8 @@ __device__ __forceinline__ void load_task(const RopeParams& p, int64_t task, int
   // loads, and the waits stay exact.
   const int64_t sv = *(p.slot_mapping ? p.slot_mapping + in.t : reinterpret_cast<const int64_t*>(p.cos_sin));
   in.slot = p.slot_mapping ? sv : -1;
-  const uint16_t* src = p.qkv + in.t * p.qkv_stride + static_cast<int64_t>(in.h) * D;
+  const uint16_t* stand_in = p.q_weight ? p.q_weight : reinterpret_cast<const uint16_t*>(p.cos_sin);
+  const uint16_t* src = real ? p.qkv + in.t * p.qkv_stride + static_cast<int64_t>(in.h) * D : stand_in;
   if constexpr (V) {
     in.a = load_row16(src + sub * E);
     in.b = load_row16(src + D / 2 + sub * E);
@@ -328,13 +335,13 @@ __global__ __launch_bounds__(kRopeThreads) void qk_norm_rope_cache_kernel(RopePa
     load_side<D, V>(p, ta, sd);
     const int64_t nb = task + stride;
     const bool more_b = nb < tasks;
-    load_task<D, V>(p, more_b ? nb : task, heads, narrow, tb);  // unconditional, as above
+    load_task<D, V>(p, more_b ? nb : task, heads, narrow, tb, more_b);  // unconditional, as above
     rope_task<Tag, D, V>(p, ta, sd);
     if (!more_b) break;
     load_side<D, V>(p, tb, sd);
     const int64_t na = nb + stride;
     const bool more_a = na < tasks;
-    load_task<D, V>(p, more_a ? na : nb, heads, narrow, ta);
+    load_task<D, V>(p, more_a ? na : nb, heads, narrow, ta, more_a);
     rope_task<Tag, D, V>(p, tb, sd);
     if (!more_a) break;
     task = na;
