@@ -1054,10 +1054,21 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   const int64_t pb = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[b]) : cb;
   const int64_t pn = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[b + 1]) - pb : Lraw;
   const int64_t PN = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[p.batch]) : N;
-  const int64_t wa = owner_wg(pb, PN, U);
-  const int64_t wb = owner_wg(pb + pn - 1, PN, U);
+  // Range v starts at position v PN / U; the owner of position x is the
+  // largest v with v PN / U <= x.  In 32 bits whenever PN (U + 1) < 2^32 (a
+  // 64-bit divide is ~10x the cost).
+  const bool narrow = PN * (U + 1) < (int64_t{1} << 32);
+  auto start = [&](int64_t v) -> int64_t {
+    return narrow ? static_cast<int64_t>(static_cast<uint32_t>(v * PN) / static_cast<uint32_t>(U)) : v * PN / U;
+  };
+  auto owner = [&](int64_t x) -> int64_t {
+    return narrow ? static_cast<int64_t>((static_cast<uint32_t>((x + 1) * U) - 1u) / static_cast<uint32_t>(PN))
+                  : owner_wg(x, PN, U);
+  };
+  const int64_t wa = owner(pb);
+  const int64_t wb = owner(pb + pn - 1);
   if (wa == wb) return;  // one range held all of it and wrote the output
-  const int s_first = wa * PN / U < pb ? 1 : 0;
+  const int s_first = start(wa) < pb ? 1 : 0;
   const int n = static_cast<int>(wb - wa + 1);
   auto row = [&](int i) -> int64_t {
     return (((wa + i) * p.num_kv_heads + kh) * 2 + (i == 0 ? s_first : 0)) * G + q;
@@ -1065,10 +1076,23 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   // Pieces of empty ranges (fewer keys than ranges) were never written.
   auto piece_lse = [&](int i) -> float {
     const int64_t v = wa + i;
-    return v * PN / U < (v + 1) * PN / U ? p.part_lse[row(i)] : -INFINITY;
+    return start(v) < start(v + 1) ? p.part_lse[row(i)] : -INFINITY;
   };
-  float M = -INFINITY;
-  for (int i = lane; i < n; i += 64) M = fmaxf(M, piece_lse(i));
+  // One round of loads for the common case: lane l's piece log2-sum-exp and
+  // the partial rows of the first eight pieces are issued together (clamped
+  // indices, weights 0 select the extra ones away).
+  const int il = min(lane, n - 1);
+  const float lse0 = p.part_lse[row(il)];
+  float pv0[8][PER];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float* po = p.part_o + row(min(j, n - 1)) * D + lane;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) pv0[j][k] = po[64 * k];
+  }
+  const float lse_l = lane < n && start(wa + lane) < start(wa + lane + 1) ? lse0 : -INFINITY;
+  float M = lse_l;
+  for (int i = lane + 64; i < n; i += 64) M = fmaxf(M, piece_lse(i));  // more than 64 pieces
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
   const float msafe = M == -INFINITY ? 0.f : M;
@@ -1078,24 +1102,30 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   float wsum = 0.f;
   for (int g = 0; g < n; g += 64) {
     const int cnt = min(64, n - g);
-    const float lse = lane < cnt ? piece_lse(g + lane) : -INFINITY;
+    const float lse = g == 0 ? lse_l : (lane < cnt ? piece_lse(g + lane) : -INFINITY);
     const float wl = lse != -INFINITY ? __builtin_amdgcn_exp2f(lse - msafe) : 0.f;
     float ws = wl;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ws += __shfl_xor(ws, m);
     wsum += ws;
-    // Eight pieces at a time: all their loads issued before the FMAs.  A
-    // piece with weight 0 (an empty range: its row was never written, or one
-    // wholly left of the window) is selected away, not multiplied.
+    // Eight pieces at a time: all their loads issued before the FMAs (the
+    // first eight were loaded above).  A piece with weight 0 (an empty range:
+    // its row was never written, or one wholly left of the window) is
+    // selected away, not multiplied.
     for (int i0 = 0; i0 < cnt; i0 += 8) {
       float wv[8], pv[8][PER];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int i = i0 + j;
         wv[j] = i < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i)) : 0.f;
-        const float* po = p.part_o + row(g + min(i, cnt - 1)) * D + lane;
+        if (g == 0 && i0 == 0) {
 #pragma unroll
-        for (int k = 0; k < PER; ++k) pv[j][k] = po[64 * k];
+          for (int k = 0; k < PER; ++k) pv[j][k] = pv0[j][k];
+        } else {
+          const float* po = p.part_o + row(g + min(i, cnt - 1)) * D + lane;
+#pragma unroll
+          for (int k = 0; k < PER; ++k) pv[j][k] = po[64 * k];
+        }
       }
 #pragma unroll
       for (int j = 0; j < 8; ++j)
