@@ -79,3 +79,48 @@ def test_noalloc_rejects_shape_beyond_scratch(device):
         ox.decode_attn(q, kc, kc, cu, bt, L, 1 / math.sqrt(D), out=out, noalloc=True)
     torch.cuda.synchronize()
     assert bool((out.float() == 7.0).all())  # nothing was launched
+
+
+def test_noalloc_under_graph_capture(device):
+    """The allocation-free entry captured into a HIP graph (torch.cuda.CUDAGraph on the
+    capture stream): the fused append + attention on a cfg3-sized batch and a plain call on
+    a small one; the graph is replayed three times with eager calls of the workspace entry
+    and host synchronisations in between, and every replay's output and caches must equal
+    the eager result bit for bit."""
+    import torch
+    import oxide_paged_kv as ox
+
+    st, kc, vc, q, app, (cu, bt) = _step(3, 200, device)
+    c = st.cfg
+    scale = 1 / math.sqrt(c.head_dim)
+    st1, kc1, vc1, q1, _, (cu1, bt1) = _step(1, 201, device)
+    scale1 = 1 / math.sqrt(st1.cfg.head_dim)
+    # Eager references: the append is idempotent (same rows to the same slots).
+    k_ref, v_ref = kc.clone(), vc.clone()
+    want = ox.decode_attn(q, k_ref, v_ref, cu, bt, st.max_seqlen_k, scale, append=app)
+    want1 = ox.decode_attn(q1, kc1, vc1, cu1, bt1, st1.max_seqlen_k, scale1)
+    out = torch.empty_like(q)
+    out1 = torch.empty_like(q1)
+    # Warm up on the side stream the capture will use (first-call device queries).
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, out=out, append=app, noalloc=True)
+        ox.decode_attn(q1, kc1, vc1, cu1, bt1, st1.max_seqlen_k, scale1, out=out1, noalloc=True)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, out=out, append=app, noalloc=True)
+        ox.decode_attn(q1, kc1, vc1, cu1, bt1, st1.max_seqlen_k, scale1, out=out1, noalloc=True)
+    for rep in range(3):
+        out.fill_(0)
+        out1.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"graph replay {rep}", flush=True)
+        assert _same(out, want) and _same(out1, want1), rep
+        assert _same(kc, k_ref) and _same(vc, v_ref), rep
+        # eager work between the replays, on the default stream
+        ox.decode_attn(q1, kc1, vc1, cu1, bt1, st1.max_seqlen_k, scale1)
+        torch.cuda.synchronize()
