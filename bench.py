@@ -361,8 +361,8 @@ def prologue_main(args) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 50; --prologue 500)")
-    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 10; --prologue 50)")
+    ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; --prologue 500)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 100; --prologue 50)")
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--layers", type=int, default=0, help="distinct layers to rotate over (0 = auto)")
     ap.add_argument("--seed", type=int, default=0)
@@ -384,9 +384,9 @@ def main() -> int:
     args = ap.parse_args()
     # A prologue call is ~0.1 ms: more of them keep the timed region near 50 ms.
     if args.steps is None:
-        args.steps = 500 if args.prologue else 50
+        args.steps = 500 if args.prologue else 200
     if args.warmup is None:
-        args.warmup = 50 if args.prologue else 10
+        args.warmup = 50 if args.prologue else 100
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -420,7 +420,7 @@ def _device_step_inputs(st, layers: int, dev, seed: int):
     return buf, q, knew, vnew, meta
 
 
-def measure_config(cfg_id: int, dev, seed: int, steps: int = 20, warmup: int = 5) -> dict:
+def measure_config(cfg_id: int, dev, seed: int, steps: int = 50, warmup: int = 20) -> dict:
     """One BASELINE config's fused append + attention call, averaged over `steps` calls
     bracketed by two HIP events on the launch stream (no events between calls), the
     steps rotating over the config's layers (cfg2: its 28 layers; others 4 layers, so no
