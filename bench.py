@@ -5,7 +5,7 @@ order (models/qwen3.rs:199-208): KV append of one new token per sequence
 (reshape_and_cache), then paged decode attention over every sequence's context --
 by default in one launch (paged_decode_attention_append), with --separate as the
 two calls of the reference.
-Default workload: BASELINE config 3 (Qwen3-8B shape, 32 q / 8 kv heads, D 128,
+Default workload: benchmark configuration 3 (Qwen3-8B shape, 32 q / 8 kv heads, D 128,
 bf16, block 256, batch 64, context U[2048, 8192], 8192-block pool), synthetic
 N(0,1) data resident in HBM, steps rotating over distinct layers of the
 [2, layers, NB, 256, 8, 128] buffer so that no step re-reads what the previous
@@ -23,7 +23,7 @@ attn_us and roofline.
 The step's K/V/q bytes come from a seeded host generator and are uploaded, so
 cpu_baseline -- the C oracle (test infrastructure, reference semantics) over
 the whole step on the same bytes -- also checks the GPU step's output
-(parity_vs_cpu).  "configs" holds every BASELINE config's fused call measured
+(parity_vs_cpu).  "configs" holds every benchmark configuration's fused call measured
 in the same run (device-generated N(0,1) data).
 """
 from __future__ import annotations
@@ -370,7 +370,7 @@ def main() -> int:
                     help="decode pass 1 (default: the library's choice by shape)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the per-config measurements of the other BASELINE configs")
+                    help="skip the per-config measurements of the other benchmark configurations")
     ap.add_argument("--separate", action="store_true",
                     help="append and attention as two calls (default: one fused call)")
     ap.add_argument("--prefill", action="store_true",
@@ -421,7 +421,7 @@ def _device_step_inputs(st, layers: int, dev, seed: int):
 
 
 def measure_config(cfg_id: int, dev, seed: int, steps: int = 50, warmup: int = 20) -> dict:
-    """One BASELINE config's fused append + attention call, averaged over `steps` calls
+    """One benchmark configuration's fused append + attention call, averaged over `steps` calls
     bracketed by two HIP events on the launch stream (no events between calls), the
     steps rotating over the config's layers (cfg2: its 28 layers; others 4 layers, so no
     call re-reads what the previous one left in the 256 MB MALL)."""
@@ -624,7 +624,7 @@ def decode_main(args) -> int:
     torch.cuda.empty_cache()
 
     if not args.no_configs and args.path == "auto" and not args.separate:
-        # Every BASELINE config's fused call, measured in this same run.
+        # Every benchmark configuration's fused call, measured in this same run.
         extra["configs"] = {f"cfg{i}": measure_config(i, dev, args.seed) for i in (1, 2, 3, 4, 5)}
 
     split = ox.split_tokens(cfg.batch, H, st.max_seqlen_k, path=path)

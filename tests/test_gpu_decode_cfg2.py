@@ -1,4 +1,4 @@
-"""BASELINE config 2 at full size: Qwen3-0.6B decode shape (16 q / 8 kv heads,
+"""Benchmark configuration 2 at full size: Qwen3-0.6B decode shape (16 q / 8 kv heads,
 D 128, bf16, block 256), batch 32, context U[512, 4096], a 4096-block pool,
 through the per-layer views of the reference's 28-layer buffer
 [2, 28, 4096, 256, 8, 128] (PagedKVCache::new / k_cache / v_cache,
