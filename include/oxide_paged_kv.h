@@ -163,7 +163,7 @@ size_t paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
                                              int64_t num_kv_heads, int64_t head_dim,
                                              int64_t max_seqlen_k);
 
-/* Tokens per KV split chosen for these arguments (256, 512 or 1024) when the
+/* Tokens per KV split chosen for these arguments (128, 256, 512 or 1024) when the
  * split grid is chosen; -1 when the wave-level stream pass is chosen (kv
  * heads dividing 8, at least ~1024 keys per stream range -- batch *
  * max_seqlen_k >= 1024 * CUs * 8 / num_kv_heads -- and at least 16 sequences

@@ -76,7 +76,7 @@ def test_workspace_and_split_policy():
 
     assert ox.split_tokens(64, 8, 8192) == -1
     assert ox.split_tokens(32, 8, 4096) == 256
-    assert ox.split_tokens(1, 1, 100) == 256
+    assert ox.split_tokens(1, 1, 100) == 128
     ws = ox.workspace_size(64, 32, 8, 128, 8192)
     assert ws >= 2 * 256 * 8 * 4 * (128 + 1) * 4
     st = ox.split_tokens(64, 8, 8192, path="split")

@@ -387,9 +387,10 @@ def test_decode_cfg5_long_context_full_size(device):
     _check_sampled(st, kc, vc, q, out, [int(lens.argmax()), int(lens.argmin())])
 
 
-@pytest.mark.parametrize("batch,ctx_hi,want_split", [(64, 4096, 512), (64, 8192, 1024), (8, 3000, 256)])
+@pytest.mark.parametrize("batch,ctx_hi,want_split", [(64, 4096, 512), (64, 8192, 1024), (16, 4096, 256),
+                                                    (8, 3000, 128)])
 def test_decode_each_split_size_sampled(device, batch, ctx_hi, want_split):
-    """One batch per split size the split grid picks (256, 512 and 1024 keys per
+    """One batch per split size the split grid picks (128, 256, 512 and 1024 keys per
     workgroup; the split path is forced, the shape policy may prefer the stream
     pass), Qwen3-8B heads, sampled sequences checked against the oracle."""
     import torch

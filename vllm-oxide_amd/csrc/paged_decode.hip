@@ -25,7 +25,7 @@
 //     key) positions, merged by paged_decode_merge_persistent.
 //
 // Pass 1 of the split grid (paged_decode_split): one workgroup of 4 waves per
-// (split, kv head, sequence); a split is 256, 512 or 1024 consecutive logical
+// (split, kv head, sequence); a split is 128, 256, 512 or 1024 consecutive logical
 // keys (choose_split_tokens), a quarter per wave, walked as 16-key tiles in
 // straight-line code with a register double buffer (tile t+1's loads are in
 // flight while tile t computes; loads past the wave's last key are clamped to
@@ -1198,11 +1198,14 @@ int64_t choose_split_tokens(int64_t batch, int64_t num_kv_heads, int64_t max_seq
   // least 4096 workgroups -- about eight per workgroup slot of the 256 CUs --
   // so that the ragged tail of the grid stays short.  Measured on MI355X:
   // Qwen3-8B B=64 ctx 2k-8k and Qwen3-32B B=16 ctx 32k-128k are fastest at
-  // 1024, Qwen3-0.6B B=32 ctx 0.5k-4k at 256.
+  // 1024, Qwen3-0.6B B=32 ctx 0.5k-4k at 256.  Grids of fewer than 2048
+  // 256-key workgroups take 128-key splits: B=4 ctx 0.3k-1k 19.4 -> 16.9 us,
+  // B=8 ctx 1-3000 18.4 -> 17.7 us (at 4096 workgroups, the 0.6B shape, the
+  // longer merge outweighs the finer grid).
   for (int64_t st : {int64_t{1024}, int64_t{512}}) {
     if (batch * num_kv_heads * ceil_div(max_seqlen_k, st) >= 4096) return st;
   }
-  return 256;
+  return batch * num_kv_heads * ceil_div(max_seqlen_k, int64_t{256}) >= 2048 ? 256 : 128;
 }
 
 dim3 split_grid(const DecodeParams& p) {
@@ -1220,7 +1223,9 @@ void launch_split(const DecodeParams& p, int64_t batch, hipStream_t s) {
   (void)batch;
   const dim3 grid = split_grid(p);
   // split_tokens = kWaves * 16 * TILES.
-  if (p.split_tokens == 256)
+  if (p.split_tokens == 128)
+    launch_tiles<Tag, D, G, 2>(p, grid, s);
+  else if (p.split_tokens == 256)
     launch_tiles<Tag, D, G, 4>(p, grid, s);
   else if (p.split_tokens == 1024)
     launch_tiles<Tag, D, G, 16>(p, grid, s);
