@@ -60,9 +60,9 @@ PaddedTable pad_block_table(const std::vector<std::vector<int32_t>>& block_table
   t.rows = block_table.size();
   for (const auto& r : block_table) t.width = std::max(t.width, r.size());
   t.data.assign(t.rows * t.width, 0);
+  // std::copy, not memcpy: an empty row's data() may be null.
   for (std::size_t b = 0; b < t.rows; ++b)
-    std::memcpy(t.data.data() + b * t.width, block_table[b].data(),
-                block_table[b].size() * sizeof(int32_t));
+    std::copy(block_table[b].begin(), block_table[b].end(), t.data.begin() + b * t.width);
   return t;
 }
 
