@@ -620,6 +620,22 @@ def decode_main(args) -> int:
     torch.cuda.synchronize()
     cbytes = 2 * nblk * 2 * (BS * H * D * 2)
     extra["stream_copy_gbps"] = round(cbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9, 1)
+    # Prefix-hit gather (gather_blocks): 1024 blocks of K and V picked at random from the
+    # same buffer into contiguous [n * BS, Hkv, D] outputs (read + write of each block).
+    ng = 1024
+    gids = torch.randperm(2 * nblk, generator=torch.Generator().manual_seed(args.seed))[:ng].int().to(dev)
+    gk = torch.empty((ng * BS, H, D), dtype=torch.bfloat16, device=dev)
+    gv = torch.empty_like(gk)
+    for _ in range(3):
+        ox.gather_blocks(cbuf[0], cbuf[1], gids, gk, gv)
+    e0.record()
+    for _ in range(10):
+        ox.gather_blocks(cbuf[0], cbuf[1], gids, gk, gv)
+    e1.record()
+    torch.cuda.synchronize()
+    gbytes = ng * 2 * 2 * (BS * H * D * 2) + 4 * ng
+    extra["gather_blocks_gbps"] = round(gbytes / (e0.elapsed_time(e1) / 10 * 1e-3) / 1e9, 1)
+    del gk, gv
     del cbuf
     torch.cuda.empty_cache()
 
