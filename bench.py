@@ -491,6 +491,9 @@ def measure_config(cfg_id: int, dev, seed: int, steps: int = 50, warmup: int = 2
         # HBM bytes the call actually moves (rocprofv3 FETCH_SIZE + WRITE_SIZE summary
         # under profiles/) over the same time.
         res["hbm_frac"] = round(traffic / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)
+        if traffic < 0.9 * nbytes:
+            res["frac_note"] = ("the algorithmic bytes include re-reads served from L2 (the shared "
+                                "prefix): hbm_frac, over the HBM bytes moved, is the roofline figure")
     if cfg.layers > 1:
         res["step_us_all_layers"] = round(us * cfg.layers, 1)
     del buf
