@@ -609,7 +609,12 @@ __device__ __forceinline__ void decode_wave_epilogue(const DecodeParams& p, int 
                                                      const floatx4 (&acc)[D / 16], bool direct,
                                                      int64_t prow_base) {
   constexpr int NDT = D / 16;
-  const int lane = threadIdx.x & 63;
+  // The lane index passes through an empty asm statement so that the per-slot
+  // addresses below are computed here, not hoisted out of the caller's loops as
+  // long-lived 64-bit values (which spill at some group sizes, and the spill
+  // reload's wait drains the tile loads in flight).
+  int lane = threadIdx.x & 63;
+  asm volatile("" : "+v"(lane));
   const int r16 = lane & 15;
   const int grp = lane >> 4;
   l_q = sum_over_lane_groups(l_q);
