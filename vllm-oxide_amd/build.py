@@ -27,6 +27,8 @@ STATIC_LIB = PKG / "liboxide_paged_kv.a"
 HOST_TEST_SRC = REPO / "tests" / "cpp" / "test_host.cpp"
 HOST_TEST_BIN = REPO / "tests" / "cpp" / "build" / "test_host"
 HOST_TEST_STAMP = HOST_TEST_BIN.with_suffix(".sources.sha256")
+# Per-kernel register, scratch and LDS use reported by the compiler for the last build.
+RESOURCES = BUILD / "kernel_resources.json"
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
@@ -43,23 +45,49 @@ def _sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.cpp")) + sorted(HOST.glob("*.cpp"))
 
 
-def _compile(src: Path) -> Path:
+def _parse_resources(text: str) -> dict:
+    """Kernel resource remarks (-Rpass-analysis=kernel-resource-usage) -> {kernel: {field: value}}."""
+    import re
+
+    out, cur = {}, None
+    for line in text.splitlines():
+        m = re.search(r"remark: Function Name: (\S+)", line)
+        if m:
+            cur = out.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"remark:\s+([A-Za-z][A-Za-z /\[\]]*?):\s+(\S+) \[-Rpass-analysis", line)
+        if m and cur is not None:
+            v = m.group(2)
+            cur[m.group(1).strip()] = int(v) if v.lstrip("-").isdigit() else v
+    return out
+
+
+def _compile(src: Path):
     obj = BUILD / (src.parent.name + "_" + src.stem + ".o")
     cmd = [HIPCC, *HIP_FLAGS, "-I", str(INCLUDE), "-I", str(CSRC), "-I", str(HOST)]
     if src.suffix == ".cpp":
         cmd += ["-x", "hip"]
+    else:
+        cmd += ["-Rpass-analysis=kernel-resource-usage"]
     cmd += ["-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{r.stdout}\n{r.stderr}")
-    return obj
+    return obj, _parse_resources(r.stderr)
 
 
 def build(verbose: bool = False) -> Path:
     BUILD.mkdir(exist_ok=True)
     srcs = _sources()
     with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
-        objs = list(ex.map(_compile, srcs))
+        results = list(ex.map(_compile, srcs))
+    objs = [o for o, _ in results]
+    import json
+
+    resources = {}
+    for _, res in results:
+        resources.update(res)
+    RESOURCES.write_text(json.dumps(resources, indent=1, sort_keys=True))
     cmd = [HIPCC, "-shared", "-fPIC", f"--offload-arch={ARCH}", "-o", str(LIB), *map(str, objs)]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
