@@ -169,6 +169,15 @@ template <>
 struct BtEntry<true> {
   typedef __attribute__((address_space(4))) const int32_t type;
 };
+// The new token's slot of sequence b (fused append), read through the constant
+// address space: a scalar load, so waiting for it does not also wait for the
+// K/V tiles in flight (a vector load here took a vmcnt(0) at every owning
+// segment's start).
+__device__ __forceinline__ int64_t new_token_slot(const DecodeParams& p, int b) {
+  typedef __attribute__((address_space(4))) const int64_t slot_t;
+  return ((slot_t*)p.slot_mapping)[b];
+}
+
 template <bool kScalar>
 __device__ __forceinline__ typename BtEntry<kScalar>::type* block_row(const DecodeParams& p, int b) {
   return (typename BtEntry<kScalar>::type*)(p.block_table + static_cast<int64_t>(b) * p.max_blocks);
@@ -395,7 +404,7 @@ __device__ __forceinline__ void decode_wave_tiles(const DecodeParams& p, char* s
                                                   float& m_q, float& l_q, floatx4 (&acc)[D / 16]) {
   uint4 kst[2][SplitShape<D, G, TILES>::VL], vst[2][SplitShape<D, G, TILES>::VL];
   const NextTile none{false, 0, 0, 0};
-  const int64_t slot_new = p.new_k != nullptr ? p.slot_mapping[b] : -1;
+  const int64_t slot_new = p.new_k != nullptr ? new_token_slot(p, b) : -1;
   decode_wave_tiles_buf<Tag, D, G, TILES, true>(p, smem, b, kh, L, w0, a, e, qb, m_q, l_q, acc, kst, vst, false, none,
                                           slot_new);
 }
@@ -768,7 +777,7 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
       load_q<D, G>(p, cur.b, kh, qb);
       // Fused append: only the piece holding key L - 1 needs the slot.
       const int64_t slot_new =
-          p.new_k != nullptr && cur.a <= cur.L - 1 && cur.L - 1 < cur.e ? p.slot_mapping[cur.b] : -1;
+          p.new_k != nullptr && cur.a <= cur.L - 1 && cur.L - 1 < cur.e ? new_token_slot(p, cur.b) : -1;
       int blk0 = cur.a & ~15;
       int ntiles = ((cur.e - 1) & ~15) / 16 - blk0 / 16 + 1;
       while (ntiles > 0) {
