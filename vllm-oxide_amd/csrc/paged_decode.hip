@@ -1035,11 +1035,19 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   const int G = p.num_heads / p.num_kv_heads;
   const int kh = h / G;
   const int q = h % G;
-  const int64_t cb = p.cu_seqlens_k[b];
-  const int64_t Lraw = max(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - cb, int64_t{0});
-  const int64_t N = p.cu_seqlens_k[p.batch];
+  // Every length this merge needs, in one round of loads: the raw prefix sums and
+  // pass 1's attended-key sums (written by pass 1 with a window; read either way,
+  // used only then).  The empty asm statement makes the compiler issue all six
+  // loads here, before any branch on them, so they share one memory latency
+  // instead of one each.
+  uint32_t c0 = p.cu_seqlens_k[b], c1 = p.cu_seqlens_k[b + 1], cn = p.cu_seqlens_k[p.batch];
+  uint32_t a0 = p.attn_cu[b], a1 = p.attn_cu[b + 1], an = p.attn_cu[p.batch];
+  asm volatile("" : "+s"(c0), "+s"(c1), "+s"(cn), "+s"(a0), "+s"(a1), "+s"(an));
+  const int64_t cb = c0;
+  const int64_t Lraw = max(static_cast<int64_t>(c1) - cb, int64_t{0});
+  const int64_t N = cn;
   uint16_t* out = static_cast<uint16_t*>(p.out) + (static_cast<int64_t>(b) * p.num_heads + h) * D;
-  if (Lraw == 0 || seq_len(p, b) == 0 || cb + Lraw > N) {
+  if (Lraw == 0 || min(Lraw, static_cast<int64_t>(p.max_seqlen_k)) == 0 || cb + Lraw > N) {
     // No keys to attend to (or an inconsistent cu_seqlens_k that pass 1 did
     // not cover): zeros; with the fused append, the first query head of each
     // kv-head group writes that head's slice of the new row.
@@ -1065,9 +1073,9 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   const int U = p.num_wgs;
   // Pass 1's key positions: raw keys, or with a window the attended ones
   // (prefix sums stored by pass 1).
-  const int64_t pb = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[b]) : cb;
-  const int64_t pn = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[b + 1]) - pb : Lraw;
-  const int64_t PN = p.window_left >= 0 ? static_cast<int64_t>(p.attn_cu[p.batch]) : N;
+  const int64_t pb = p.window_left >= 0 ? static_cast<int64_t>(a0) : cb;
+  const int64_t pn = p.window_left >= 0 ? static_cast<int64_t>(a1) - pb : Lraw;
+  const int64_t PN = p.window_left >= 0 ? static_cast<int64_t>(an) : N;
   // Range v starts at position v PN / U; the owner of position x is the
   // largest v with v PN / U <= x.  In 32 bits whenever PN (U + 1) < 2^32 (a
   // 64-bit divide is ~10x the cost).
