@@ -196,22 +196,23 @@ def prefill_cpu_baseline(seed: int, threads: int, min_seconds: float = 10.0) -> 
             "sample": f"one {L}-token prompt, Qwen3-8B heads, fp32-accumulated, {reps} reps in {dt:.1f} s"}
 
 
-def prefill_main(args) -> int:
+def measure_prefill(dev, B: int, Lq: int, P: int, seed: int, steps: int, warmup: int) -> dict:
+    """One paged prefill attention call (B prompts of Lq new tokens behind P cached tokens,
+    Qwen3-8B heads) timed with two HIP events bracketing `steps` calls on the launch
+    stream, the calls alternating between two layers' caches."""
     import torch
 
     import oxide_paged_kv as ox
 
-    dev = torch.device("cuda:0")
-    B, Lq, P = args.prompts, args.prompt_len, args.prefix
     Lk = Lq + P
     Hq, Hkv, D, BS = 32, 8, 128, 256
     nb = (Lk + BS - 1) // BS
-    g = torch.Generator(device=dev).manual_seed(args.seed)
+    g = torch.Generator(device=dev).manual_seed(seed)
     layers = 2
     kc = torch.randn((layers, B * nb, BS, Hkv, D), generator=g, device=dev).bfloat16()
     vc = torch.randn((layers, B * nb, BS, Hkv, D), generator=g, device=dev).bfloat16()
     q = torch.randn((layers, B * Lq, Hq, D), generator=g, device=dev).bfloat16()
-    perm = torch.randperm(B * nb, generator=torch.Generator().manual_seed(args.seed)).int()
+    perm = torch.randperm(B * nb, generator=torch.Generator().manual_seed(seed)).int()
     table = perm.view(B, nb).to(dev)
     cuq = (torch.arange(B + 1, dtype=torch.int32) * Lq).to(dev)
     cuk = (torch.arange(B + 1, dtype=torch.int32) * Lk).to(dev)
@@ -222,40 +223,54 @@ def prefill_main(args) -> int:
         ox.prefill_attn(q[i % layers], kc[i % layers], vc[i % layers], cuq, cuk, Lq, Lk, scale, table,
                         None, out)
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         call(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
-    for i in range(args.steps):
+    for i in range(steps):
         call(i)
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    us = e0.elapsed_time(e1) / args.steps * 1e3
+    us = e0.elapsed_time(e1) / steps * 1e3
     flops = B * prefill_flops(Lq, Lk, Hq, D)
     tflops = flops / (us * 1e-6) / 1e12
+    del kc, vc, q, out
+    torch.cuda.empty_cache()
+    return {"workload": f"prefill-qwen3-8b-{B}x{Lq}" + (f"-prefix{P}" if P else ""),
+            "prompts": B, "prompt_len": Lq, "prefix": P, "num_heads": Hq, "num_kv_heads": Hkv,
+            "head_dim": D, "block_size": BS, "kernel": "paged_prefill_attn", "calls": steps,
+            "call_us": round(us, 2), "wall_ms_per_call": round(wall * 1e3 / steps, 4),
+            "tflops": round(tflops, 2), "algorithmic_flops": flops,
+            "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "peak_tflops": MFMA_BF16_PEAK_TFLOPS}
+
+
+def prefill_main(args) -> int:
+    import torch
+
+    dev = torch.device("cuda:0")
+    m = measure_prefill(dev, args.prompts, args.prompt_len, args.prefix, args.seed, args.steps, args.warmup)
     res = {
         "metric": "paged prefill attention TFLOP/s (causal, Qwen3-8B heads)",
-        "value": round(tflops, 2),
+        "value": m["tflops"],
         "unit": "TFLOP/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "ms_per_step": m["wall_ms_per_call"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic N(0,1) Q/K/V, seeded random block tables",
-        "config": {"workload": f"prefill-qwen3-8b-{B}x{Lq}" + (f"-prefix{P}" if P else ""),
-                   "prompts": B, "prompt_len": Lq, "prefix": P, "num_heads": Hq, "num_kv_heads": Hkv,
-                   "head_dim": D, "block_size": BS},
-        "call_us": round(us, 2),
-        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS,
-                     "unit": "TFLOP/s", "frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
-                     "kernel": "paged_prefill_attn", "algorithmic_flops": flops},
+        "config": {k: m[k] for k in ("workload", "prompts", "prompt_len", "prefix", "num_heads", "num_kv_heads",
+                                     "head_dim", "block_size")},
+        "call_us": m["call_us"],
+        "roofline": {"bound": "mfma", "achieved": m["tflops"], "peak": MFMA_BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": m["frac"], "traffic": None,
+                     "kernel": "paged_prefill_attn", "algorithmic_flops": m["algorithmic_flops"]},
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = prefill_cpu_baseline(args.seed, min(16, os.cpu_count() or 1))
@@ -295,15 +310,17 @@ def prologue_cpu_baseline(seed: int, min_seconds: float = 10.0) -> dict:
             "kind": "port", "sample": f"{T} tokens, Qwen3-8B heads, scalar C, {reps} reps in {dt:.1f} s"}
 
 
-def prologue_main(args) -> int:
+def measure_prologue(dev, T: int, seed: int, steps: int, warmup: int) -> dict:
+    """One qk_norm_rope_and_cache call over T tokens (Qwen3-8B heads) timed with two HIP
+    events bracketing `steps` calls on the launch stream, the calls rotating over four
+    layers' qkv rows."""
     import torch
 
     import oxide_paged_kv as ox
 
-    dev = torch.device("cuda:0")
-    T, Hq, Hkv, D, BS = args.tokens, 32, 8, 128, 256
+    Hq, Hkv, D, BS = 32, 8, 128, 256
     layers = 4
-    g = torch.Generator(device=dev).manual_seed(args.seed)
+    g = torch.Generator(device=dev).manual_seed(seed)
     qkv = torch.randn((layers, T, (Hq + 2 * Hkv) * D), generator=g, device=dev).bfloat16()
     w = (1 + 0.1 * torch.randn((2, D), generator=g, device=dev)).bfloat16()
     cs = ox.rope_cos_sin_cache(32768, D, 1_000_000.0, dev)
@@ -325,32 +342,44 @@ def prologue_main(args) -> int:
         ox.qk_norm_rope_and_cache(layer_qkv[i % layers], Hq, Hkv, w[0], w[1], 1e-6, cs, pos, kc, vc, slots,
                                   q_out=q_out)
 
-    for i in range(args.warmup):
+    for i in range(warmup):
         call(i)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     e0.record()
-    for i in range(args.steps):
+    for i in range(steps):
         call(i)
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    us = e0.elapsed_time(e1) / args.steps * 1e3
+    us = e0.elapsed_time(e1) / steps * 1e3
     nbytes = prologue_bytes(T, Hq, Hkv, D)
     gbps = nbytes / (us * 1e-6) / 1e9
+    del qkv, kc, vc, q_out
+    torch.cuda.empty_cache()
+    return {"workload": f"prologue-qwen3-8b-{T}tok", "tokens": T, "num_heads": Hq, "num_kv_heads": Hkv,
+            "head_dim": D, "kernel": "qk_norm_rope_cache_kernel", "calls": steps, "call_us": round(us, 2),
+            "wall_ms_per_call": round(wall * 1e3 / steps, 4), "gbps": round(gbps, 1),
+            "algorithmic_bytes": nbytes, "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "traffic": _profile_value(PROLOGUE_PROFILE, "traffic_bytes_per_call") if T == 16384 else None}
+
+
+def prologue_main(args) -> int:
+    import torch
+
+    dev = torch.device("cuda:0")
+    m = measure_prologue(dev, args.tokens, args.seed, args.steps, args.warmup)
     res = {
         "metric": "fused q/k RMSNorm + RoPE + KV append GB/s (Qwen3-8B heads)",
-        "value": round(gbps, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True, "scaling": "weak",
+        "value": m["gbps"], "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": m["wall_ms_per_call"], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic N(0,1) qkv rows, random slots; positions 0..4095 per prompt (T > 256) or random",
-        "config": {"workload": f"prologue-qwen3-8b-{T}tok", "tokens": T, "num_heads": Hq, "num_kv_heads": Hkv,
-                   "head_dim": D},
-        "call_us": round(us, 2),
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4),
-                     "traffic": _profile_value(PROLOGUE_PROFILE, "traffic_bytes_per_call") if T == 16384 else None,
-                     "kernel": "qk_norm_rope_cache_kernel", "algorithmic_bytes": nbytes},
+        "config": {k: m[k] for k in ("workload", "tokens", "num_heads", "num_kv_heads", "head_dim")},
+        "call_us": m["call_us"],
+        "roofline": {"bound": "hbm", "achieved": m["gbps"], "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": m["frac"], "traffic": m["traffic"],
+                     "kernel": "qk_norm_rope_cache_kernel", "algorithmic_bytes": m["algorithmic_bytes"]},
     }
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = prologue_cpu_baseline(args.seed)
@@ -573,15 +602,28 @@ def decode_main(args) -> int:
     # recorded between the steps): in the fused mode a step is exactly one
     # attention call, so the bracketed time over the steps is the call's average
     # duration, back to back.
+    # The same few ms of device work ahead of the bracket as the per-config entries queue
+    # (two fills of a 4 GiB buffer): the host has then enqueued the first timed calls
+    # before the GPU reaches them, and the first calls after an idle GPU (which run
+    # ~2 % slower) fall inside the fills, so the figure does not depend on --warmup.
+    filler = torch.empty(1 << 31, dtype=torch.int16, device=dev)
+    torch.cuda.synchronize()
+    f0 = torch.cuda.Event(enable_timing=True)
     b0, b1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
+    f0.record()
+    filler.fill_(1)
+    filler.fill_(2)
     b0.record()
     for i in range(args.steps):
         step(args.warmup + i)
     b1.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
+    # Wall clock over the timed steps: host time from before the fills to the end of the
+    # last step, less the fills' own device time (f0 -> b0).
+    wall = time.perf_counter() - t0 - f0.elapsed_time(b0) * 1e-3
     bracket_us = b0.elapsed_time(b1) / args.steps * 1e3
+    del filler
     evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(args.steps)]
     for i in range(args.steps):
         step(args.warmup + i, evs[i])
@@ -652,6 +694,17 @@ def decode_main(args) -> int:
     if not args.no_configs and args.path == "auto" and not args.separate:
         # Every benchmark configuration's fused call, measured in this same run.
         extra["configs"] = {f"cfg{i}": measure_config(i, dev, args.seed) for i in (1, 2, 3, 4, 5)}
+        # The next-row kernels of the same layer, measured in the same run (no CPU baselines
+        # here; `--prefill` / `--prologue` run them alone with theirs): paged prefill
+        # attention at two prompt shapes (matrix-core roofline) and the fused q/k norm +
+        # RoPE + KV append over 16k tokens (HBM roofline).
+        extra["prefill"] = {m["workload"]: m for m in
+                            (measure_prefill(dev, 4, 4096, 0, args.seed, 20, 5),
+                             measure_prefill(dev, 16, 1024, 0, args.seed, 20, 5))}
+        extra["prologue"] = measure_prologue(dev, 16384, args.seed, 200, 20)
+        if extra["prologue"]["traffic"]:
+            extra["prologue"]["traffic_over_algorithmic"] = round(
+                extra["prologue"]["traffic"] / extra["prologue"]["algorithmic_bytes"], 4)
 
     split = ox.split_tokens(cfg.batch, H, st.max_seqlen_k, path=path)
     res = {

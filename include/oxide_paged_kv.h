@@ -316,8 +316,19 @@ void build_decode_metadata_device(const uint32_t* context_lens, const int32_t* b
  * before it is read).  A shape whose first pass needs more than the array
  * (its partial rows, their log-sum-exps and, windowed, the attended-key
  * prefix sums) is rejected with OXIDE_ERR_SCRATCH_TOO_SMALL and launches
- * nothing; Qwen3 shapes with up to 16 query heads per kv head at head_dim 128
- * fit at any batch the stream pass takes.  Every call on one device shares
+ * nothing.  The stream pass (the shape policy's choice for batches of 16 or
+ * more sequences with long contexts) needs 2 rows per wave slot and query of the
+ * group (2 x CUs x 16 x G rows): Qwen3 shapes with up to 16 query heads per kv
+ * head at head_dim 128 fit at any batch it takes.  The split grid (smaller
+ * batches) needs a row per (sequence, query head, split): with
+ * rows = batch x num_heads x ceil(max_seqlen_k / split), split =
+ * paged_decode_attention_split_tokens(...) when it returns > 0, the call fits
+ * when round_up(rows x head_dim x 4, 256) + round_up(rows x 4, 256) <= 48 MiB
+ * (at 1024-key splits, head_dim 128: rows <= 97,541, e.g. 15 sequences of 64k
+ * keys at 128 query heads do not fit).  A caller that captures graphs can check
+ * a shape with that bound before capture.  The first call on a device resolves
+ * the array's address; it may itself be made under graph capture (the query
+ * enqueues nothing).  Every call on one device shares
  * that device's array: calls that overlap in time on one device (two streams,
  * two threads) race and give wrong results; calls ordered on one stream do not.
  * Other arguments and results as for paged_decode_attention_append.

@@ -312,7 +312,8 @@ extern "C" {
         dst: *mut c_void,
         n: i64,
         seed: u64,
-        stream: HipStream,
+        /// the generator's stream id (one independent sequence per id), not a HIP stream
+        stream: u64,
         dtype: c_int,
         threads: c_int,
     ) -> c_int;

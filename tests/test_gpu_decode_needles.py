@@ -36,11 +36,22 @@ pytestmark = pytest.mark.gpu
 PATHS = {1: "split", 2: "persistent", 3: "stream"}
 
 
+def _config(cfg_id):
+    from oxide_paged_kv.workload import CONFIGS, DecodeConfig
+
+    if cfg_id in CONFIGS:
+        return CONFIGS[cfg_id]
+    # Small batches that the shape policy gives 128-key splits (grids of fewer than 2048
+    # 256-key workgroups), without and with a window.
+    return {"b4-w300": DecodeConfig("b4-ctx0.3k-1k-w300", 32, 8, 128, 4, 300, 1000, 64, window_left=300),
+            "b8": DecodeConfig("b8-ctx1-3000", 32, 8, 128, 8, 1, 3000, 128)}[cfg_id]
+
+
 def _inputs(cfg_id, seed, device):
     import torch
-    from oxide_paged_kv.workload import CONFIGS, make_decode_step
+    from oxide_paged_kv.workload import make_decode_step
 
-    st = make_decode_step(CONFIGS[cfg_id], seed=seed)
+    st = make_decode_step(_config(cfg_id), seed=seed)
     c = st.cfg
     g = torch.Generator(device=device).manual_seed(seed)
     shape = (st.pool_blocks, c.block_size, c.num_kv_heads, c.head_dim)
@@ -68,7 +79,7 @@ def _stream_range_starts(st, device):
 
 
 def _needle_positions(st, device, rng):
-    """Up to 9 distinct key positions per sequence inside its attended keys."""
+    """Up to 13 distinct key positions per sequence inside its attended keys."""
     starts, lo = _stream_range_starts(st, device)
     out = []
     for b, L in enumerate(st.context_lens.astype(np.int64)):
@@ -77,7 +88,7 @@ def _needle_positions(st, device, rng):
         if len(starts[b]):
             x = int(rng.choice(starts[b]))
             pos |= {x - 1, x}
-        for step in (1024, 256):
+        for step in (1024, 512, 256, 128):
             m = [k for k in range(((a + step) // step) * step, int(L) - 1, step)]
             if m:
                 x = int(rng.choice(m))
@@ -146,17 +157,22 @@ def _needle_want(st, q, needles):
     return want
 
 
-@pytest.mark.parametrize("cfg_id", [3, 4, 5])
+@pytest.mark.parametrize("cfg_id", [1, "b4-w300", "b8", 3, 4, 5])
 def test_decode_needles_full_size(device, cfg_id):
-    """Full-size cfg3, cfg4 (window 4096) and cfg5: needles on the piece boundaries of
-    every first pass; fused append (the new token is a needle) then plain attention,
-    through each of the three passes."""
+    """Full-size cfg1, cfg3, cfg4 (window 4096) and cfg5, and two small batches whose
+    shape policy takes 128-key splits (one windowed): needles on the piece boundaries of
+    every first pass (128/256/512/1024-key splits and blocks, stream ranges); fused
+    append (the new token is a needle) then plain attention, through each of the three
+    passes."""
     import torch
     import oxide_paged_kv as ox
 
-    st, kc0, vc0, g = _inputs(cfg_id, 90 + cfg_id, device)
+    seed = 90 + (cfg_id if isinstance(cfg_id, int) else len(cfg_id))
+    st, kc0, vc0, g = _inputs(cfg_id, seed, device)
     c = st.cfg
-    rng = np.random.default_rng(cfg_id)
+    if not isinstance(cfg_id, int):
+        assert ox.split_tokens(c.batch, c.num_kv_heads, st.max_seqlen_k) == 128
+    rng = np.random.default_rng(seed)
     q, knew, vnew, needles = _plant_needles(st, kc0, vc0, g, rng, device)
     want = _needle_want(st, q, needles)
     print(f"cfg{cfg_id} needles per sequence: {[len(n[0]) for n in needles]}", flush=True)

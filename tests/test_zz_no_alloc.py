@@ -124,3 +124,56 @@ def test_noalloc_under_graph_capture(device):
         # eager work between the replays, on the default stream
         ox.decode_attn(q1, kc1, vc1, cu1, bt1, st1.max_seqlen_k, scale1)
         torch.cuda.synchronize()
+
+
+_CAPTURE_FIRST = r'''
+import math, sys
+sys.path[:0] = [{repo!r}, {pkg!r}]
+import numpy as np
+import torch
+import oxide_paged_kv as ox
+from oxide_paged_kv.workload import CONFIGS, make_decode_step
+
+dev = torch.device("cuda:0")
+st = make_decode_step(CONFIGS[{cfg}], seed=300)
+c = st.cfg
+g = torch.Generator(device=dev).manual_seed(300)
+shape = (st.pool_blocks, c.block_size, c.num_kv_heads, c.head_dim)
+kc = torch.randn(shape, generator=g, device=dev).bfloat16()
+vc = torch.randn(shape, generator=g, device=dev).bfloat16()
+q = torch.randn((c.batch, c.num_heads, c.head_dim), generator=g, device=dev).bfloat16()
+cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(dev)
+bt = torch.from_numpy(st.block_table).to(dev)
+scale = 1 / math.sqrt(c.head_dim)
+out = torch.empty_like(q)
+ox.load()  # the library is loaded (its code objects registered) before the capture
+torch.cuda.synchronize()
+# The library's first call in this process is the one being captured.
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, out=out, noalloc=True)
+for rep in range(2):
+    out.fill_(0)
+    graph.replay()
+    torch.cuda.synchronize()
+    want = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16)), rep
+print("capture-first ok", flush=True)
+'''
+
+
+@pytest.mark.parametrize("cfg_id", [1, 3], ids=["split-grid-cfg1", "stream-cfg3"])
+def test_noalloc_first_call_under_graph_capture(cfg_id):
+    """In a fresh process whose first library call is the allocation-free entry under
+    HIP graph capture (no warm-up: the device queries and the scratch address lookup
+    run during the capture), the replays equal the workspace entry bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    repo = Path(__file__).resolve().parent.parent
+    code = _CAPTURE_FIRST.format(repo=str(repo), pkg=str(repo / "vllm-oxide_amd"), cfg=cfg_id)
+    print(f"capture-first subprocess cfg{cfg_id}", flush=True)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "capture-first ok" in r.stdout, r.stdout[-2000:] + r.stderr[-4000:]

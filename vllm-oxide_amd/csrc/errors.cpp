@@ -28,6 +28,7 @@ int device_cu_count() {
   std::atomic<int>& n = cache[dev % kMaxDevices];
   int v = n.load(std::memory_order_relaxed);
   if (v == 0) {
+    RelaxedCaptureScope relaxed;
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
     n.store(v, std::memory_order_relaxed);
   }

@@ -21,6 +21,21 @@ void check_launch();
 // Compute units of the current device (cached per device; 256 when the query fails).
 int device_cu_count();
 
+// First-use device queries (CU counts, occupancies, the static scratch's address)
+// run inside this scope: the calling thread's stream-capture mode is relaxed for its
+// lifetime, so a first call made under HIP graph capture (global mode) may query the
+// device -- the queries enqueue nothing on any stream.
+struct RelaxedCaptureScope {
+  hipStreamCaptureMode saved = hipStreamCaptureModeRelaxed;
+  bool ok;
+  RelaxedCaptureScope() : ok(hipThreadExchangeStreamCaptureMode(&saved) == hipSuccess) {}
+  ~RelaxedCaptureScope() {
+    if (ok) (void)hipThreadExchangeStreamCaptureMode(&saved);
+  }
+  RelaxedCaptureScope(const RelaxedCaptureScope&) = delete;
+  RelaxedCaptureScope& operator=(const RelaxedCaptureScope&) = delete;
+};
+
 inline int dtype_size(int dtype) {
   switch (dtype) {
     case OXIDE_DTYPE_F16:

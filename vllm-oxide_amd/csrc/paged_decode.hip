@@ -1284,6 +1284,7 @@ void launch_persistent(DecodeParams p, hipStream_t s) {
   if (hipGetDevice(&dev) != hipSuccess) dev = 0;
   int occ = occ_cache[dev % kMaxDevices].load(std::memory_order_relaxed);
   if (occ == 0) {
+    oxide::RelaxedCaptureScope relaxed;
     int n = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, paged_decode_persistent<Tag, D, G>, kThreads, 0) !=
         hipSuccess)
@@ -1650,6 +1651,7 @@ void* scratch_ptr() {
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
   ScratchSlot& slot = g_scratch[dev];
   std::call_once(slot.once, [&slot] {
+    oxide::RelaxedCaptureScope relaxed;  // the first call may come under graph capture
     void* ptr = nullptr;
     slot.err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
     if (slot.err == hipSuccess) slot.ptr = ptr;
