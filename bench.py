@@ -58,15 +58,18 @@ def _profile_value(path, key: str):
     return None
 
 
-# Decode pass 1 as reported by split_tokens(): > 0 split grid, 0 persistent, -1 stream.
-PASS1_NAMES = {"split": "split grid", "persistent": "persistent balanced", "stream": "wave-level stream"}
+# Decode pass 1 as reported by split_tokens(): > 0 split grid, 0 persistent, -1 stream, -2 rows.
+PASS1_NAMES = {"split": "split grid", "persistent": "persistent balanced", "stream": "wave-level stream",
+               "rows": "whole-row stream"}
 PASS1_KERNELS = {"split": "paged_decode_split + paged_decode_merge",
                  "persistent": "paged_decode_persistent + paged_decode_merge_persistent",
-                 "stream": "paged_decode_stream + paged_decode_merge_stream"}
+                 "stream": "paged_decode_stream + paged_decode_merge_stream",
+                 "rows": "paged_decode_rows + paged_decode_merge_stream"}
 
 
 def _pass1(split_tokens: int) -> str:
-    return "split" if split_tokens > 0 else ("persistent" if split_tokens == 0 else "stream")
+    return ("split" if split_tokens > 0 else "persistent" if split_tokens == 0 else
+            "stream" if split_tokens == -1 else "rows")
 
 
 def profiled_traffic(config: int, separate: bool):
@@ -395,7 +398,7 @@ def main() -> int:
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--layers", type=int, default=0, help="distinct layers to rotate over (0 = auto)")
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--path", choices=["auto", "split", "persistent", "stream"], default="auto",
+    ap.add_argument("--path", choices=["auto", "split", "persistent", "stream", "rows"], default="auto",
                     help="decode pass 1 (default: the library's choice by shape)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-configs", action="store_true",
@@ -510,7 +513,8 @@ def measure_config(cfg_id: int, dev, seed: int, steps: int = 50, warmup: int = 2
     us = e0.elapsed_time(e1) / steps * 1e3
     nbytes = st.attn_bytes() + st.append_bytes()
     gbps = nbytes / (us * 1e-6) / 1e9
-    split = ox.split_tokens(cfg.batch, cfg.num_kv_heads, st.max_seqlen_k)
+    split = ox.split_tokens(cfg.batch, cfg.num_kv_heads, st.max_seqlen_k, num_heads=cfg.num_heads,
+                            head_dim=cfg.head_dim, page_block_size=cfg.block_size)
     traffic = profiled_traffic(cfg_id, False)
     res.update({"workload": cfg.name, "pass1": PASS1_NAMES[_pass1(split)], "attn_us": round(us, 2),
                 "algorithmic_bytes": nbytes, "attn_gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
@@ -706,7 +710,8 @@ def decode_main(args) -> int:
             extra["prologue"]["traffic_over_algorithmic"] = round(
                 extra["prologue"]["traffic"] / extra["prologue"]["algorithmic_bytes"], 4)
 
-    split = ox.split_tokens(cfg.batch, H, st.max_seqlen_k, path=path)
+    split = ox.split_tokens(cfg.batch, H, st.max_seqlen_k, path=path, num_heads=cfg.num_heads, head_dim=D,
+                            page_block_size=BS)
     res = {
         "metric": "paged-decode attn KV-read GB/s (% HBM peak) + append GB/s, Qwen3-8B shape",
         "value": round(value, 2),

@@ -182,7 +182,9 @@ int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
  * tuning and tests.  The choice is an argument of this call only: the library
  * keeps no state between calls.  path: 0 = by shape (as the plain entries),
  * 1 = the split grid, 2 = the persistent pass, 3 = the stream pass where the
- * kv heads divide 8 (else the persistent pass); anything else is
+ * kv heads divide 8 (else the persistent pass), 4 = the row pass where the shape
+ * allows it (head_dim 128, 8 kv heads, 32 query heads, power-of-two pages, at
+ * most 1024 sequences; else as 3); anything else is
  * OXIDE_ERR_INVALID_ARGUMENT.  Results agree within rounding; the workspace
  * size is the same for every path.
  */
@@ -200,6 +202,15 @@ void paged_decode_attention_path(int path, void* out, const void* q, const void*
  * by shape; codes outside 0..3 read as 0).  No reference counterpart. */
 int64_t paged_decode_attention_path_split_tokens(int path, int64_t batch, int64_t num_kv_heads,
                                                  int64_t max_seqlen_k);
+
+/* The first pass paged_decode_attention_path(path, ...) runs on these arguments
+ * (path 0 = by shape, as the plain entries; codes outside 0..4 read as 0): the
+ * split size (> 0) for the split grid, 0 for the persistent pass, -1 for the
+ * stream pass, -2 for the row pass.  Unlike the two queries above it knows the
+ * query heads, head size and page size, which the row pass depends on.  No
+ * reference counterpart. */
+int64_t paged_decode_attention_pass1(int path, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                     int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k);
 
 /*
  * Prefill attention over the paged cache.  Replaces the general (seqlen_q >= 1)

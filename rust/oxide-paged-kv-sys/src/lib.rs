@@ -182,6 +182,18 @@ extern "C" {
         max_seqlen_k: i64,
     ) -> i64;
 
+    /// First pass run by paged_decode_attention_path(path, ...): split size (> 0), 0 persistent,
+    /// -1 stream, -2 row pass.
+    pub fn paged_decode_attention_pass1(
+        path: c_int,
+        batch: i64,
+        num_heads: i64,
+        num_kv_heads: i64,
+        head_dim: i64,
+        page_block_size: i64,
+        max_seqlen_k: i64,
+    ) -> i64;
+
     /// Prefill (seqlen_q >= 1) call of flash_attn_varlen_paged_windowed over the paged cache, causal,
     /// masks aligned bottom-right; cached prefix keys are read in place.
     pub fn paged_prefill_attention(

@@ -66,13 +66,18 @@ CASES = [
     (2, 12, 4, 64, 256, 20, [900, 31], -1, "f16"),                      # G=3, D=64
     (2, 24, 4, 128, 256, 20, [1500, 256], -1, "bf16"),                  # G=6
     (3, 16, 8, 128, 256, 10, [3, 1, 2], -1, "bf16"),                    # fewer keys than stream ranges
+    # Qwen3-8B heads (the row pass's shape) with small pages, f16, windows, empty sequences
+    (5, 32, 8, 128, 16, 300, [0, 10, 0, 1, 300], -1, "f16"),
+    (3, 32, 8, 128, 32, 200, [2000, 700, 101], 100, "bf16"),
+    (2, 32, 8, 128, 256, 20, [600, 5], 0, "bf16"),
 ]
 
 
-@pytest.fixture(params=[1, 2, 3], ids=["split", "persistent", "stream"])
+@pytest.fixture(params=[1, 2, 3, 4], ids=["split", "persistent", "stream", "rows"])
 def decode_path(request):
     """Runs a test once per pass-1 path (split grid, persistent balanced pass,
-    wave-level stream pass)."""
+    wave-level stream pass, whole-row pass -- the stream pass for shapes the row
+    pass does not take)."""
     return request.param
 
 
@@ -343,6 +348,14 @@ def test_decode_path_policy(device):
     assert ox.split_tokens(64, 8, 8192, path="stream") == -1
     assert ox.split_tokens(16, 16, 131072, path="stream") == 0   # kv heads not dividing 8
     assert ox.split_tokens(64, 8, 8192) == -1
+    # The row pass: only when forced, and only for its shape (else the stream pass).
+    assert ox.split_tokens(64, 8, 8192, num_heads=32) == -1
+    assert ox.split_tokens(64, 8, 8192, path="rows", num_heads=32) == -2
+    assert ox.split_tokens(64, 8, 8192, path="rows", num_heads=32, page_block_size=48) == -1
+    assert ox.split_tokens(64, 8, 8192, path="rows", num_heads=16) == -1
+    assert ox.split_tokens(64, 8, 8192, path="rows", num_heads=32, head_dim=64) == -1
+    assert ox.split_tokens(2000, 8, 8192, path="rows", num_heads=32) == -1  # beyond its LDS table
+    assert ox.split_tokens(32, 8, 4096, num_heads=16) == 256
 
 
 @pytest.mark.parametrize("cfg_id", [3, 4, 5])
@@ -358,7 +371,7 @@ def test_decode_paths_agree_full_size(device, cfg_id):
     cu = torch.from_numpy(st.cu_seqlens_k.view(np.int32)).to(device)
     bt = torch.from_numpy(st.block_table).to(device)
     outs = []
-    for path in (1, 2, 3):
+    for path in (1, 2, 3, 4):
         print(f"cfg{cfg_id} path {path}", flush=True)
         outs.append(to_f32(ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, 1 / math.sqrt(c.head_dim),
                                           None if c.window_left < 0 else c.window_left, path=path)))
@@ -366,6 +379,8 @@ def test_decode_paths_agree_full_size(device, cfg_id):
     assert_attn_close(outs[2], outs[0])
     assert_attn_scaled(outs[1], outs[0], label="persistent vs split")
     assert_attn_scaled(outs[2], outs[0], label="stream vs split")
+    assert_attn_close(outs[3], outs[0])
+    assert_attn_scaled(outs[3], outs[0], label="rows vs split")
     lens = st.context_lens.astype(np.int64)
     for o in outs[1:]:
         _check_sampled(st, kc, vc, q, o, [int(lens.argmax()), int(lens.argmin())], c.window_left)
@@ -456,10 +471,11 @@ def test_decode_fused_append_equals_append_then_attend(device, case, decode_path
     assert np.array_equal(to_bits(v2), to_bits(v1))
 
 
-@pytest.mark.parametrize("cfg_id", [3, 4, 5])
-def test_decode_fused_append_full_size(device, cfg_id):
+@pytest.mark.parametrize("cfg_id,path", [(3, 0), (4, 0), (5, 0), (3, 4), (4, 4)],
+                         ids=["cfg3", "cfg4", "cfg5", "cfg3-rows", "cfg4-rows"])
+def test_decode_fused_append_full_size(device, cfg_id, path):
     """Full-size cfg3 / cfg4 (window 4096) / cfg5 step: fused append + attention
-    equals the two calls."""
+    equals the two calls (by shape, and through the row pass)."""
     import torch
     import oxide_paged_kv as ox
 
@@ -475,8 +491,8 @@ def test_decode_fused_append_full_size(device, cfg_id):
     k2, v2 = kc.clone(), vc.clone()
     ox.reshape_and_cache(kn, vn, kc, vc, sm)
     w = None if c.window_left < 0 else c.window_left
-    want = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, w)
-    got = ox.decode_attn(q, k2, v2, cu, bt, st.max_seqlen_k, scale, w, append=(kn, vn, sm))
+    want = ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, w, path=path)
+    got = ox.decode_attn(q, k2, v2, cu, bt, st.max_seqlen_k, scale, w, append=(kn, vn, sm), path=path)
     torch.cuda.synchronize()
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
     assert torch.equal(k2.view(torch.int16), kc.view(torch.int16))

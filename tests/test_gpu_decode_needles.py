@@ -33,7 +33,7 @@ from helpers import assert_attn_close, assert_attn_scaled, to_bits, to_f32
 
 pytestmark = pytest.mark.gpu
 
-PATHS = {1: "split", 2: "persistent", 3: "stream"}
+PATHS = {1: "split", 2: "persistent", 3: "stream", 4: "rows"}
 
 
 def _config(cfg_id):

@@ -1,0 +1,157 @@
+// Shared state and helpers of the paged decode passes (paged_decode.hip,
+// paged_decode_rows.hip): the launch parameters, sequence lengths, the 16-byte
+// non-temporal K/V load, the scalar reads of the block table and the new token's
+// slot, and the attended-key prefix sums of windowed batches.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+
+#include "oxide_common.hpp"
+
+namespace oxide {
+
+struct DecodeParams {
+  const void* q;
+  const void* k;
+  const void* v;
+  const uint32_t* cu_seqlens_k;
+  const int32_t* block_table;
+  float* part_o;    // [B, Hq, max_splits, D]
+  float* part_lse;  // [B, Hq, max_splits]
+  void* out;        // [B, Hq, D]
+  // Fused append (paged_decode_attention_append), null otherwise: the new
+  // token's K/V [B, Hkv, D] and its slot per sequence.
+  const void* new_k;
+  const void* new_v;
+  const int64_t* slot_mapping;
+  int64_t max_blocks;
+  int num_blocks;
+  int max_seqlen_k;
+  int num_heads;
+  int num_kv_heads;
+  int block_size;
+  int window_left;
+  int split_tokens;
+  int max_splits;
+  int batch;
+  int num_wgs;  // balanced paths: key ranges per kv head (persistent, stream, rows)
+  int stream_deep;  // stream path: two tiles in flight per wave (see launch_stream)
+  float scale_log2;
+  // Stream and row paths with a window: prefix sums of the attended keys per
+  // sequence (written by pass 1's first workgroup, read by the merge).
+  uint32_t* attn_cu;
+};
+
+// First pass of the row path (paged_decode_rows.hip): launches it for a shape
+// rows_path_ok accepts and returns true; p.num_wgs is set to its key ranges.
+bool launch_rows_pass1(DecodeParams& p, bool bf16, hipStream_t s);
+// Shapes the row path takes: head_dim 128, 8 kv heads, group size 4, and
+// power-of-two pages, and batches whose sequence boundaries fit its LDS table.
+bool rows_path_ok(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t block_size);
+// Partial rows the row path writes at most (two per range, kv head and query).
+int64_t rows_partial_rows(int64_t num_heads);
+
+}  // namespace oxide
+
+namespace {
+
+using oxide::DecodeParams;
+
+constexpr int kXcds = 8;  // MI355X: workgroup i runs on XCD i % 8
+
+// One 16-byte K/V chunk.
+// Non-temporal: K/V are streamed once per call (measured on MI355X: plain
+// loads cost 4-8 % on every decode path).
+__device__ __forceinline__ uint4 load_kv16(const uint16_t* p) {
+  const oxide::u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const oxide::u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Keys of sequence b.  Lengths beyond max_seqlen_k (a caller error) are
+// clamped so that neither pass can index past the workspace or the block-table
+// row; a decreasing cu_seqlens_k reads as an empty sequence.
+__device__ __forceinline__ int seq_len(const DecodeParams& p, int b) {
+  const int64_t n = static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - p.cu_seqlens_k[b];
+  return static_cast<int>(n < 0 ? 0 : (n > p.max_seqlen_k ? p.max_seqlen_k : n));
+}
+
+// The block table is not written while a kernel runs.  Read through the
+// constant address space (kScalar), wave-uniform lookups compile to scalar
+// loads, counted apart from the K/V vector loads, and a wave keeps two tiles in
+// flight.  Read as ordinary memory they are vector loads: the lookup for tile
+// t + 1, issued after tile t's loads, completes after them (vector loads
+// complete in issue order), so tile t + 1's loads wait for tile t and a wave
+// keeps one tile in flight -- which the stream pass over long ranges prefers
+// (measured on MI355X; see launch_stream).
+template <bool kScalar>
+struct BtEntry {
+  typedef const int32_t type;
+};
+template <>
+struct BtEntry<true> {
+  typedef __attribute__((address_space(4))) const int32_t type;
+};
+// The new token's slot of sequence b (fused append), read through the constant
+// address space: a scalar load, so waiting for it does not also wait for the
+// K/V tiles in flight (a vector load here took a vmcnt(0) at every owning
+// segment's start).
+__device__ __forceinline__ int64_t new_token_slot(const DecodeParams& p, int b) {
+  typedef __attribute__((address_space(4))) const int64_t slot_t;
+  return ((slot_t*)p.slot_mapping)[b];
+}
+
+template <bool kScalar>
+__device__ __forceinline__ typename BtEntry<kScalar>::type* block_row(const DecodeParams& p, int b) {
+  return (typename BtEntry<kScalar>::type*)(p.block_table + static_cast<int64_t>(b) * p.max_blocks);
+}
+
+// Largest b in [0, batch) with cu[b] <= key (cu non-decreasing).
+__device__ __forceinline__ int find_seq(const uint32_t* cu, int batch, int64_t key) {
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (static_cast<int64_t>(cu[mid]) <= key)
+      lo = mid;
+    else
+      hi = mid - 1;
+  }
+  return lo;
+}
+
+// Windowed balanced passes: the attended keys of sequence b are [lo_b, L_b)
+// with L_b = seq_len, lo_b = max(0, L_b - 1 - window_left); cu[0..batch]
+// receives their exclusive prefix sums and lo[b] the lo_b (a workgroup scan in
+// LDS: each thread sums a run of sequences, the run totals are scanned, the runs
+// written).  Called by every thread of a workgroup of kT threads.
+template <int kT>
+__device__ __forceinline__ void attended_prefix(const DecodeParams& p, uint32_t* cu, int* lo) {
+  __shared__ uint32_t run_sum[kT];
+  const int t = threadIdx.x;
+  const int per = (p.batch + kT - 1) / kT;
+  const int b0 = min(p.batch, t * per), b1 = min(p.batch, b0 + per);
+  uint32_t s = 0;
+  for (int b = b0; b < b1; ++b) {
+    const int L = seq_len(p, b);
+    const int l0 = max(0, L - 1 - p.window_left);
+    lo[b] = l0;
+    s += static_cast<uint32_t>(L - l0);
+  }
+  run_sum[t] = s;
+  __syncthreads();
+  for (int off = 1; off < kT; off <<= 1) {  // inclusive scan of the run totals
+    const uint32_t v = t >= off ? run_sum[t - off] : 0u;
+    __syncthreads();
+    run_sum[t] += v;
+    __syncthreads();
+  }
+  uint32_t x = t > 0 ? run_sum[t - 1] : 0u;
+  for (int b = b0; b < b1; ++b) {
+    cu[b] = x;
+    x += static_cast<uint32_t>(seq_len(p, b) - lo[b]);
+  }
+  if (t == kT - 1) cu[p.batch] = run_sum[kT - 1];
+}
+
+}  // namespace

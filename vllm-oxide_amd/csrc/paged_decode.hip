@@ -56,65 +56,17 @@
 #include <algorithm>
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "cdna4_tile.hpp"
+#include "decode_common.hpp"
 #include "oxide_common.hpp"
 
 namespace {
 
 
-// One 16-byte K/V chunk.
-// Non-temporal: K/V are streamed once per call (measured on MI355X: plain
-// loads cost 4-8 % on every decode path).
-__device__ __forceinline__ uint4 load_kv16(const uint16_t* p) {
-  const oxide::u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const oxide::u32x4*>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-
-
-struct DecodeParams {
-  const void* q;
-  const void* k;
-  const void* v;
-  const uint32_t* cu_seqlens_k;
-  const int32_t* block_table;
-  float* part_o;    // [B, Hq, max_splits, D]
-  float* part_lse;  // [B, Hq, max_splits]
-  void* out;        // [B, Hq, D]
-  // Fused append (paged_decode_attention_append), null otherwise: the new
-  // token's K/V [B, Hkv, D] and its slot per sequence.
-  const void* new_k;
-  const void* new_v;
-  const int64_t* slot_mapping;
-  int64_t max_blocks;
-  int num_blocks;
-  int max_seqlen_k;
-  int num_heads;
-  int num_kv_heads;
-  int block_size;
-  int window_left;
-  int split_tokens;
-  int max_splits;
-  int batch;
-  int num_wgs;  // persistent path: workgroups sharing the flattened key space
-  int stream_deep;  // stream path: two tiles in flight per wave (see launch_stream)
-  float scale_log2;
-  // Stream path with a window: prefix sums of the attended keys per sequence
-  // (written by pass 1's first workgroup, read by the merge).
-  uint32_t* attn_cu;
-};
-
-// Keys of sequence b.  Lengths beyond max_seqlen_k (a caller error) are
-// clamped so that neither pass can index past the workspace or the block-table
-// row; a decreasing cu_seqlens_k reads as an empty sequence.
-__device__ __forceinline__ int seq_len(const DecodeParams& p, int b) {
-  const int64_t n = static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - p.cu_seqlens_k[b];
-  return static_cast<int>(n < 0 ? 0 : (n > p.max_seqlen_k ? p.max_seqlen_k : n));
-}
-
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kXcds = 8;  // MI355X: workgroup i runs on XCD i % 8
 
 // Work item (split, kv head, sequence) of this workgroup; false for padding.
 // 1-D grid, XCD-grouped: a unit u = (seq, split) is pinned to XCD u % 8 and its
@@ -153,36 +105,6 @@ __device__ __forceinline__ bool decode_work_item(const DecodeParams& p, int& spl
 // reads land on disjoint banks.
 
 // Shared layout constants of pass 1.
-// The block table is not written while a kernel runs.  Read through the
-// constant address space (kScalar), wave-uniform lookups compile to scalar
-// loads, counted apart from the K/V vector loads, and a wave keeps two tiles in
-// flight.  Read as ordinary memory they are vector loads: the lookup for tile
-// t + 1, issued after tile t's loads, completes after them (vector loads
-// complete in issue order), so tile t + 1's loads wait for tile t and a wave
-// keeps one tile in flight -- which the stream pass over long ranges prefers
-// (measured on MI355X; see launch_stream).
-template <bool kScalar>
-struct BtEntry {
-  typedef const int32_t type;
-};
-template <>
-struct BtEntry<true> {
-  typedef __attribute__((address_space(4))) const int32_t type;
-};
-// The new token's slot of sequence b (fused append), read through the constant
-// address space: a scalar load, so waiting for it does not also wait for the
-// K/V tiles in flight (a vector load here took a vmcnt(0) at every owning
-// segment's start).
-__device__ __forceinline__ int64_t new_token_slot(const DecodeParams& p, int b) {
-  typedef __attribute__((address_space(4))) const int64_t slot_t;
-  return ((slot_t*)p.slot_mapping)[b];
-}
-
-template <bool kScalar>
-__device__ __forceinline__ typename BtEntry<kScalar>::type* block_row(const DecodeParams& p, int b) {
-  return (typename BtEntry<kScalar>::type*)(p.block_table + static_cast<int64_t>(b) * p.max_blocks);
-}
-
 template <int D, int G, int TILES>
 struct SplitShape {
   static constexpr int KK = D / 32;
@@ -522,19 +444,6 @@ __device__ __forceinline__ int64_t owner_wg(int64_t x, int64_t n, int w) {
   return ((x + 1) * w - 1) / n;  // largest v with v * n / w <= x
 }
 
-// Largest b in [0, batch) with cu[b] <= key (cu non-decreasing).
-__device__ __forceinline__ int find_seq(const uint32_t* cu, int batch, int64_t key) {
-  int lo = 0, hi = batch - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (static_cast<int64_t>(cu[mid]) <= key)
-      lo = mid;
-    else
-      hi = mid - 1;
-  }
-  return lo;
-}
-
 template <class Tag, int D, int G>
 __global__ __launch_bounds__(kThreads, 2) void paged_decode_persistent(DecodeParams p) {
   constexpr int TILES = 16;
@@ -648,40 +557,6 @@ __device__ __forceinline__ void decode_wave_epilogue(const DecodeParams& p, int 
   }
 }
 
-// Windowed stream pass: the attended keys of sequence b are [lo_b, L_b) with
-// L_b = seq_len, lo_b = max(0, L_b - 1 - window_left); cu[0..batch] receives
-// their exclusive prefix sums and lo[b] the lo_b (a workgroup scan in LDS:
-// each thread sums a run of sequences, the run totals are scanned, the runs
-// written).  Called by every thread of the workgroup.
-__device__ __forceinline__ void stream_attended_prefix(const DecodeParams& p, uint32_t* cu, int* lo) {
-  constexpr int kT = 64 * kStreamWaves;
-  __shared__ uint32_t run_sum[kT];
-  const int t = threadIdx.x;
-  const int per = (p.batch + kT - 1) / kT;
-  const int b0 = min(p.batch, t * per), b1 = min(p.batch, b0 + per);
-  uint32_t s = 0;
-  for (int b = b0; b < b1; ++b) {
-    const int L = seq_len(p, b);
-    const int l0 = max(0, L - 1 - p.window_left);
-    lo[b] = l0;
-    s += static_cast<uint32_t>(L - l0);
-  }
-  run_sum[t] = s;
-  __syncthreads();
-  for (int off = 1; off < kT; off <<= 1) {  // inclusive scan of the run totals
-    const uint32_t v = t >= off ? run_sum[t - off] : 0u;
-    __syncthreads();
-    run_sum[t] += v;
-    __syncthreads();
-  }
-  uint32_t x = t > 0 ? run_sum[t - 1] : 0u;
-  for (int b = b0; b < b1; ++b) {
-    cu[b] = x;
-    x += static_cast<uint32_t>(seq_len(p, b) - lo[b]);
-  }
-  if (t == kT - 1) cu[p.batch] = run_sum[kT - 1];
-}
-
 template <class Tag, int D, int G, bool kDeep>
 __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(DecodeParams p) {
   typedef SplitShape<D, G, 16> S16;
@@ -702,7 +577,7 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   if (!windowed) {
     for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) cu[i] = p.cu_seqlens_k[i];
   } else {
-    stream_attended_prefix(p, cu, win_lo);
+    attended_prefix<64 * kStreamWaves>(p, cu, win_lo);
   }
   __syncthreads();  // the last barrier: before any wave can leave
   // The merge's copy of the sums (after the barrier: every thread's runs are in).
@@ -1177,7 +1052,7 @@ using oxide::device_cu_count;
 // B=16 ctx 32k-128k: 883 vs 953 us); slower below (Qwen3-8B B=64 ctx 2k-8k,
 // Qwen3-0.6B B=32 ctx 0.5k-4k), where the split grid's many short workgroups
 // hide their start-up and the XCD-aware order helps more than the balance.
-enum DecodePath { kPathSplit = 1, kPathPersistent = 2, kPathStream = 3 };
+enum DecodePath { kPathSplit = 1, kPathPersistent = 2, kPathStream = 3, kPathRows = 4 };
 
 // The stream pass needs the kv heads to divide its 8 waves per workgroup and
 // the sequence boundaries to fit its LDS table.
@@ -1204,7 +1079,11 @@ int64_t stream_keys_per_range(int64_t batch, int64_t num_kv_heads, int64_t max_s
 }
 
 // forced: the caller's choice (paged_decode_attention_path), 0 = by shape.
-DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k, int forced) {
+// rows_ok: the shape fits the row pass (oxide::rows_path_ok); callers that do not
+// know the query heads pass false.
+DecodePath choose_path(int64_t batch, int64_t num_kv_heads, int64_t max_seqlen_k, int forced, bool rows_ok = false) {
+  if (forced == kPathRows && rows_ok) return kPathRows;
+  if (forced == kPathRows) forced = kPathStream;
   if (forced == kPathStream && !stream_ok(batch, num_kv_heads)) return kPathPersistent;
   if (forced >= kPathSplit && forced <= kPathStream) return static_cast<DecodePath>(forced);
   const int64_t cus = device_cu_count();
@@ -1373,6 +1252,13 @@ bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hip
     if (head_dim == 64) return dispatch_persistent<Tag, 64>(p, group, s);
     return false;
   }
+  if (p.split_tokens == -2) {  // row pass (shape checked by the caller) + the stream merge
+    DecodeParams q = p;
+    oxide::launch_rows_pass1(q, std::is_same<Tag, Bf16Tag>::value, s);
+    hipLaunchKernelGGL((paged_decode_merge_stream<Tag, 128>),
+                       dim3(static_cast<unsigned>(q.num_heads), static_cast<unsigned>(q.batch)), dim3(64), 0, s, q);
+    return true;
+  }
   if (p.split_tokens < 0) {
     if (head_dim == 128) return dispatch_stream<Tag, 128>(p, group, s);
     if (head_dim == 64) return dispatch_stream<Tag, 64>(p, group, s);
@@ -1430,9 +1316,21 @@ int64_t attn_cu_offset(int64_t batch, int64_t num_heads, int64_t num_kv_heads, i
 
 extern "C" int64_t paged_decode_attention_path_split_tokens(int path, int64_t batch, int64_t num_kv_heads,
                                                             int64_t max_seqlen_k) {
-  switch (choose_path(batch, num_kv_heads, max_seqlen_k, path >= 0 && path <= 3 ? path : 0)) {
+  switch (choose_path(batch, num_kv_heads, max_seqlen_k, path >= 0 && path <= 4 ? path : 0)) {
     case kPathPersistent: return 0;
     case kPathStream: return -1;
+    case kPathRows: return -2;
+    default: return choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
+  }
+}
+
+extern "C" int64_t paged_decode_attention_pass1(int path, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                                int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k) {
+  const bool rows_ok = oxide::rows_path_ok(batch, num_heads, num_kv_heads, head_dim, page_block_size);
+  switch (choose_path(batch, num_kv_heads, max_seqlen_k, path >= 0 && path <= 4 ? path : 0, rows_ok)) {
+    case kPathPersistent: return 0;
+    case kPathStream: return -1;
+    case kPathRows: return -2;
     default: return choose_split_tokens(batch, num_kv_heads, max_seqlen_k);
   }
 }
@@ -1490,7 +1388,9 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
     oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
     return;
   }
-  const DecodePath path = max_seqlen_k > 0 ? choose_path(batch, num_kv_heads, max_seqlen_k, forced_path) : kPathSplit;
+  const bool rows_ok = oxide::rows_path_ok(batch, num_heads, num_kv_heads, head_dim, page_block_size);
+  const DecodePath path =
+      max_seqlen_k > 0 ? choose_path(batch, num_kv_heads, max_seqlen_k, forced_path, rows_ok) : kPathSplit;
   const bool persistent = path != kPathSplit;
   const int64_t st = max_seqlen_k > 0 ? choose_split_tokens(batch, num_kv_heads, max_seqlen_k) : 1;
   const int64_t max_splits = max_seqlen_k > 0 ? ceil_div(max_seqlen_k, st) : 0;
@@ -1528,7 +1428,7 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
   p.block_size = static_cast<int>(page_block_size);
   p.window_left = window_left < 0 ? -1 : window_left;
   // 0 selects the persistent path, -1 the stream path.
-  p.split_tokens = path == kPathPersistent ? 0 : path == kPathStream ? -1 : static_cast<int>(st);
+  p.split_tokens = path == kPathPersistent ? 0 : path == kPathStream ? -1 : path == kPathRows ? -2 : static_cast<int>(st);
   p.stream_deep = path == kPathStream &&
                   (stream_keys_per_range(batch, num_kv_heads, max_seqlen_k) < 1536 || window_left >= 0);
   if (max_seqlen_k > 0) p.attn_cu = reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + cu_off);
@@ -1611,7 +1511,7 @@ extern "C" void paged_decode_attention_path(
     int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k,
     int32_t window_left, float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
     void* stream) {
-  if (path < 0 || path > 3) {
+  if (path < 0 || path > 4) {
     oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
     return;
   }

@@ -96,18 +96,24 @@ def workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
                                                                  head_dim, max_seqlen_k))
 
 
-def split_tokens(batch: int, num_kv_heads: int, max_seqlen_k: int, path: int | str = 0) -> int:
+def split_tokens(batch: int, num_kv_heads: int, max_seqlen_k: int, path: int | str = 0,
+                 num_heads: int | None = None, head_dim: int = 128, page_block_size: int = 256) -> int:
     """Tokens per KV split of the decode pass 1; 0 for the persistent balanced pass, -1 for
-    the wave-level stream pass.  path: as for decode_attn (0 / "auto" = by shape)."""
+    the wave-level stream pass, -2 for the row pass (only reported when num_heads is given:
+    the row pass depends on the query heads).  path: as for decode_attn (0 / "auto" = by
+    shape)."""
     L = _lib.load()
     path = DECODE_PATHS[path] if isinstance(path, str) else int(path)
+    if num_heads is not None:
+        return int(L.paged_decode_attention_pass1(path, batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                                                  max_seqlen_k))
     if path == 0:
         return int(L.paged_decode_attention_split_tokens(batch, num_kv_heads, max_seqlen_k))
     return int(L.paged_decode_attention_path_split_tokens(path, batch, num_kv_heads, max_seqlen_k))
 
 
 # First-pass names of paged_decode_attention_path.
-DECODE_PATHS = {"auto": 0, "split": 1, "persistent": 2, "stream": 3}
+DECODE_PATHS = {"auto": 0, "split": 1, "persistent": 2, "stream": 3, "rows": 4}
 
 
 def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
