@@ -11,7 +11,10 @@
 // 512 KiB, so a pair is pure HBM streaming.  Each workgroup owns one pair and
 // a 16 KiB slice of it (256 lanes x 4 x 128-bit vectors) and moves the slice
 // of K and of V, keeping 8 independent 128-bit loads in flight per lane before
-// the stores.  blockIdx.x walks the slices of a pair, blockIdx.y the pairs, so
+// the stores; loads and stores are non-temporal (measured on MI355X, 2048 pairs of
+// 1 MiB K+V: 751 -> 715 us with non-temporal stores, 6.0 TB/s read+write; 1024
+// random blocks gathered: 393 -> 368 us, 5.8 TB/s; 8 vectors per lane instead of 4,
+// or K and V in separate workgroups, no faster).  blockIdx.x walks the slices of a pair, blockIdx.y the pairs, so
 // a launch has pairs x (block_bytes / 16 KiB) workgroups: 4096 for 128 pairs of 512 KiB,
 // enough to cover all 256 CUs many times over.  The copy is bitwise, so every
 // dtype takes the same path; strides that are not a multiple of 16 bytes fall
@@ -63,10 +66,10 @@ __global__ __launch_bounds__(kThreads) void block_copy_vec16(
         vr[u] = __builtin_nontemporal_load(vs + base + u * kThreads);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) kd[base + u * kThreads] = kr[u];
+    for (int u = 0; u < kUnroll; ++u) __builtin_nontemporal_store(kr[u], kd + base + u * kThreads);
     if (vs) {
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) vd[base + u * kThreads] = vr[u];
+      for (int u = 0; u < kUnroll; ++u) __builtin_nontemporal_store(vr[u], vd + base + u * kThreads);
     }
   } else {
     for (int u = 0; u < kUnroll; ++u) {
