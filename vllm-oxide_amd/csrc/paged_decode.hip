@@ -1302,7 +1302,8 @@ int64_t persistent_rows(int64_t num_heads, int64_t num_kv_heads) {
 }
 
 int64_t partial_rows_max(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t max_seqlen_k) {
-  return std::max(split_rows(batch, num_heads, num_kv_heads, max_seqlen_k), persistent_rows(num_heads, num_kv_heads));
+  return std::max({split_rows(batch, num_heads, num_kv_heads, max_seqlen_k), persistent_rows(num_heads, num_kv_heads),
+                   oxide::rows_partial_rows(num_heads)});
 }
 // The windowed stream pass's attended-key prefix sums follow the partial rows of
 // the largest layout.
@@ -1395,7 +1396,9 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
   const int64_t st = max_seqlen_k > 0 ? choose_split_tokens(batch, num_kv_heads, max_seqlen_k) : 1;
   const int64_t max_splits = max_seqlen_k > 0 ? ceil_div(max_seqlen_k, st) : 0;
   const WorkspaceLayout wl = workspace_layout(
-      persistent ? persistent_rows(num_heads, num_kv_heads) : split_rows(batch, num_heads, num_kv_heads, max_seqlen_k),
+      path == kPathRows ? oxide::rows_partial_rows(num_heads)
+      : persistent      ? persistent_rows(num_heads, num_kv_heads)
+                        : split_rows(batch, num_heads, num_kv_heads, max_seqlen_k),
       head_dim);
   const int64_t cu_off = max_seqlen_k <= 0 ? 0
                          : compact_ws ? wl.total

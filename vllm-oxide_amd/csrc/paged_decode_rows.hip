@@ -5,10 +5,12 @@
 // crates/vllm-oxide/src/attention/flash_attn.rs:52-67, window_right = 0,
 // seqlen_q = 1); its pieces are merged by paged_decode_merge_stream.
 //
-// Why: on MI355X a read-only kernel streaming the cfg3 batch's K/V as whole
-// 1 KiB-per-instruction rows runs ~5 % faster than one that streams per-head
-// 256-byte slices (83 % vs 79 % of 8 TB/s), and every wave then reads two
-// contiguous 512 KiB pages (K and V) per 256 keys.
+// Why it exists: a read-only probe of the Qwen3-8B B=64 batch read whole
+// 1 KiB-per-instruction token rows ~5 % faster than per-head 256-byte slices,
+// and every wave here reads two contiguous 512 KiB pages (K and V) per 256 keys.
+// Measured in the full kernel on MI355X it runs at the stream pass's rate (its
+// loads alone ~1 % faster, its arithmetic costs that back), so the shape policy
+// never picks it; paged_decode_attention_path(4, ...) runs it on request.
 //
 // Work split: the batch's keys (with a window: its attended keys) are laid end to
 // end and cut into one equal range per workgroup (one 8-wave workgroup per CU).  A
@@ -423,6 +425,8 @@ bool rows_path_ok(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_
          block_size >= 2 && (block_size & (block_size - 1)) == 0;
 }
 
+// Two rows (the range's first and last sequence) per key range -- one range per
+// workgroup, at most one workgroup per CU -- and query head.
 int64_t rows_partial_rows(int64_t num_heads) { return 2 * static_cast<int64_t>(device_cu_count()) * num_heads; }
 
 bool launch_rows_pass1(DecodeParams& p, bool bf16, hipStream_t s) {
