@@ -203,6 +203,40 @@ void paged_decode_attention_path(int path, void* out, const void* q, const void*
 int64_t paged_decode_attention_path_split_tokens(int path, int64_t batch, int64_t num_kv_heads,
                                                  int64_t max_seqlen_k);
 
+/*
+ * Paged decode attention (key, value and slot_mapping all NULL) or the fused
+ * append + attention (all three given) of a batch whose block-table rows share
+ * their leading entries -- a common prompt prefix cached once (the BlockPool's
+ * prefix sharing) -- computed as a cascade: the shared keys are attended once for
+ * every sequence (matrix cores, all (sequence, query head) rows against each
+ * shared K/V tile), the remaining keys per sequence by the decode stream pass, and
+ * the two merged with log-sum-exp weights.  Same results as
+ * paged_decode_attention(_append) within rounding; no reference counterpart (the
+ * reference reads the shared blocks once per sequence).
+ * shared_blocks_hint: an upper bound on the leading entries shared by every row
+ * (0 = no cascade: the plain entries run).  The kernels find the actual count on
+ * the device (identical block ids in every row, and at most (L_b - 1) / block_size
+ * for every sequence), so a wrong hint costs time, never correctness.  Shapes the
+ * stream pass does not take (kv heads not dividing 8, more than 4096 sequences)
+ * run the plain entries.  workspace: paged_decode_attention_shared_prefix_workspace_size
+ * bytes.  Other arguments as for paged_decode_attention_append.
+ */
+void paged_decode_attention_shared_prefix(void* out, const void* q, const void* key, const void* value,
+                                          const int64_t* slot_mapping, void* k_cache, void* v_cache,
+                                          const uint32_t* cu_seqlens_k, const int32_t* block_table,
+                                          int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
+                                          int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                                          int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left,
+                                          float softmax_scale, int64_t shared_blocks_hint, void* workspace,
+                                          size_t workspace_bytes, int dtype, void* stream);
+
+/* Bytes of workspace paged_decode_attention_shared_prefix needs (at least
+ * paged_decode_attention_workspace_size, so the fallback fits too). */
+size_t paged_decode_attention_shared_prefix_workspace_size(int64_t batch, int64_t num_heads,
+                                                           int64_t num_kv_heads, int64_t head_dim,
+                                                           int64_t page_block_size, int64_t max_seqlen_k,
+                                                           int64_t shared_blocks_hint);
+
 /* The first pass paged_decode_attention_path(path, ...) runs on these arguments
  * (path 0 = by shape, as the plain entries; codes outside 0..4 read as 0): the
  * split size (> 0) for the split grid, 0 for the persistent pass, -1 for the

@@ -182,6 +182,46 @@ extern "C" {
         max_seqlen_k: i64,
     ) -> i64;
 
+    /// Cascaded decode for batches whose block-table rows share leading entries (a cached
+    /// prompt prefix): the shared keys attended once for all sequences, the rest per sequence;
+    /// key/value/slot_mapping all null = no append.  No reference counterpart.
+    pub fn paged_decode_attention_shared_prefix(
+        out: *mut c_void,
+        q: *const c_void,
+        key: *const c_void,
+        value: *const c_void,
+        slot_mapping: *const i64,
+        k_cache: *mut c_void,
+        v_cache: *mut c_void,
+        cu_seqlens_k: *const u32,
+        block_table: *const i32,
+        max_blocks_per_seq: i64,
+        num_blocks: i64,
+        batch: i64,
+        num_heads: i64,
+        num_kv_heads: i64,
+        head_dim: i64,
+        page_block_size: i64,
+        max_seqlen_k: i64,
+        window_left: i32,
+        softmax_scale: f32,
+        shared_blocks_hint: i64,
+        workspace: *mut c_void,
+        workspace_bytes: usize,
+        dtype: c_int,
+        stream: HipStream,
+    );
+
+    pub fn paged_decode_attention_shared_prefix_workspace_size(
+        batch: i64,
+        num_heads: i64,
+        num_kv_heads: i64,
+        head_dim: i64,
+        page_block_size: i64,
+        max_seqlen_k: i64,
+        shared_blocks_hint: i64,
+    ) -> usize;
+
     /// First pass run by paged_decode_attention_path(path, ...): split size (> 0), 0 persistent,
     /// -1 stream, -2 row pass.
     pub fn paged_decode_attention_pass1(

@@ -42,7 +42,49 @@ struct DecodeParams {
   // Stream and row paths with a window: prefix sums of the attended keys per
   // sequence (written by pass 1's first workgroup, read by the merge).
   uint32_t* attn_cu;
+  // Cascaded call (paged_decode_attention_shared_prefix), null otherwise: the
+  // number of leading block-table entries every sequence shares, written by the
+  // shared-prefix pass.  The stream pass then attends only keys from
+  // shared_blocks[0] * block_size on, writes whole sequences as partials too (at
+  // split pre_splits of the prefix rows), and the merge adds the prefix pass's
+  // partial rows: row pre_row0 + s * batch * Hq + b * Hq + h for split s.
+  const int* shared_blocks;
+  int64_t pre_row0;
+  int pre_splits;
+  int split_keys;
+  int64_t whole_row0;  // pre_row0 + pre_splits * batch * Hq; -1 without a cascade
 };
+
+// Shared-prefix pass of a cascaded decode call (paged_prefill.hip): attention of
+// every (sequence, query head) row of the decode batch over the leading
+// block-table entries all rows share (found on the device, at most shared_hint),
+// as partial rows per key split.
+struct DecodePrefixArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const uint32_t* cu_seqlens_k;
+  const int32_t* block_table;
+  int64_t max_blocks;
+  int num_blocks;
+  int batch;
+  int num_heads;
+  int num_kv_heads;
+  int head_dim;
+  int block_size;
+  int max_seqlen_k;
+  int window_left;
+  float scale_log2;
+  float* part_o;
+  float* part_lse;
+  int64_t pre_row0;
+  int pre_splits;
+  int split_keys;
+  int shared_hint;
+  int* shared_out;
+  bool bf16;
+};
+bool launch_decode_prefix(const DecodePrefixArgs& a, hipStream_t s);
 
 // First pass of the row path (paged_decode_rows.hip): launches it for a shape
 // rows_path_ok accepts and returns true; p.num_wgs is set to its key ranges.
@@ -120,13 +162,14 @@ __device__ __forceinline__ int find_seq(const uint32_t* cu, int batch, int64_t k
   return lo;
 }
 
-// Windowed balanced passes: the attended keys of sequence b are [lo_b, L_b)
-// with L_b = seq_len, lo_b = max(0, L_b - 1 - window_left); cu[0..batch]
+// Windowed (or cascaded) balanced passes: the attended keys of sequence b are
+// [lo_b, L_b) with L_b = seq_len, lo_b = max(key_floor, L_b - 1 - window_left)
+// (the window term only with a window; lo_b <= L_b); cu[0..batch]
 // receives their exclusive prefix sums and lo[b] the lo_b (a workgroup scan in
 // LDS: each thread sums a run of sequences, the run totals are scanned, the runs
 // written).  Called by every thread of a workgroup of kT threads.
 template <int kT>
-__device__ __forceinline__ void attended_prefix(const DecodeParams& p, uint32_t* cu, int* lo) {
+__device__ __forceinline__ void attended_prefix(const DecodeParams& p, uint32_t* cu, int* lo, int key_floor = 0) {
   __shared__ uint32_t run_sum[kT];
   const int t = threadIdx.x;
   const int per = (p.batch + kT - 1) / kT;
@@ -134,7 +177,7 @@ __device__ __forceinline__ void attended_prefix(const DecodeParams& p, uint32_t*
   uint32_t s = 0;
   for (int b = b0; b < b1; ++b) {
     const int L = seq_len(p, b);
-    const int l0 = max(0, L - 1 - p.window_left);
+    const int l0 = min(L, max(key_floor, p.window_left >= 0 ? L - 1 - p.window_left : 0));
     lo[b] = l0;
     s += static_cast<uint32_t>(L - l0);
   }

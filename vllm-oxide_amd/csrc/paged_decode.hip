@@ -523,9 +523,13 @@ constexpr int kStreamCuLds = 4096;
 // Per-wave epilogue of a segment: query slot s < G of lane group 0 holds
 // query s; acc[dt][j] of lane l is slot 4 (l / 16) + j, dim 16 dt + l % 16.
 template <class Tag, int D, int G>
+// whole: the segment is the sequence's whole (attended) key range; otherwise a
+// piece, written to range u's slot (first ? 0 : 1).  A cascaded call writes whole
+// sequences as partials too (the merge adds the shared prefix), at prefix split
+// pre_splits of their rows.
 __device__ __forceinline__ void decode_wave_epilogue(const DecodeParams& p, int b, int kh, float m_q, float l_q,
-                                                     const floatx4 (&acc)[D / 16], bool direct,
-                                                     int64_t prow_base) {
+                                                     const floatx4 (&acc)[D / 16], bool whole, bool first,
+                                                     int64_t u) {
   constexpr int NDT = D / 16;
   // The lane index passes through an empty asm statement so that the per-slot
   // addresses below are computed here, not hoisted out of the caller's loops as
@@ -533,6 +537,12 @@ __device__ __forceinline__ void decode_wave_epilogue(const DecodeParams& p, int 
   // reload's wait drains the tile loads in flight).
   int lane = threadIdx.x & 63;
   asm volatile("" : "+v"(lane));
+  // One 64-bit argument carries the cascade (-1: none), so the pass holds no more
+  // scalar state across its tile loop than without it.
+  const bool cascade = p.whole_row0 >= 0;
+  const bool direct = whole && !cascade;
+  const int64_t prow_base = cascade && whole ? p.whole_row0 + static_cast<int64_t>(b) * p.num_heads + kh * G
+                                             : ((u * p.num_kv_heads + kh) * 2 + (first ? 0 : 1)) * G;
   const int r16 = lane & 15;
   const int grp = lane >> 4;
   l_q = sum_over_lane_groups(l_q);
@@ -573,11 +583,13 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   // sequence, laid end to end, cu holding their prefix sums and win_lo the lo_b
   // -- so keys before a window start weigh nothing in the balance.
   __shared__ int win_lo[kStreamCuLds];
-  const bool windowed = p.window_left >= 0;
+  // A cascaded call attends only the keys past the shared prefix here (its
+  // prefix pass wrote the number of shared blocks): ranges over attended keys.
+  const bool windowed = p.window_left >= 0 || p.shared_blocks != nullptr;
   if (!windowed) {
     for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) cu[i] = p.cu_seqlens_k[i];
   } else {
-    attended_prefix<64 * kStreamWaves>(p, cu, win_lo);
+    attended_prefix<64 * kStreamWaves>(p, cu, win_lo, p.shared_blocks ? *p.shared_blocks * p.block_size : 0);
   }
   __syncthreads();  // the last barrier: before any wave can leave
   // The merge's copy of the sums (after the barrier: every thread's runs are in).
@@ -672,8 +684,7 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
         ntiles -= step;
       }
     }
-    decode_wave_epilogue<Tag, D, G>(p, cur.b, kh, m_q, l_q, acc, cur.whole,
-                                    ((static_cast<int64_t>(u) * Hkv + kh) * 2 + (first_seg ? 0 : 1)) * G);
+    decode_wave_epilogue<Tag, D, G>(p, cur.b, kh, m_q, l_q, acc, cur.whole, first_seg, u);
     first_seg = false;
     cur = nxt;
   }
@@ -946,11 +957,14 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
     return;
   }
   const int U = p.num_wgs;
-  // Pass 1's key positions: raw keys, or with a window the attended ones
-  // (prefix sums stored by pass 1).
-  const int64_t pb = p.window_left >= 0 ? static_cast<int64_t>(a0) : cb;
-  const int64_t pn = p.window_left >= 0 ? static_cast<int64_t>(a1) - pb : Lraw;
-  const int64_t PN = p.window_left >= 0 ? static_cast<int64_t>(an) : N;
+  // Cascaded call: the prefix pass's partial rows join pass 1's pieces.
+  const bool cascade = p.shared_blocks != nullptr;
+  // Pass 1's key positions: raw keys, or with a window (or a cascade) the attended
+  // ones (prefix sums stored by pass 1).
+  const bool attended = p.window_left >= 0 || cascade;
+  const int64_t pb = attended ? static_cast<int64_t>(a0) : cb;
+  const int64_t pn = attended ? static_cast<int64_t>(a1) - pb : Lraw;
+  const int64_t PN = attended ? static_cast<int64_t>(an) : N;
   // Range v starts at position v PN / U; the owner of position x is the
   // largest v with v PN / U <= x.  In 32 bits whenever PN (U + 1) < 2^32 (a
   // 64-bit divide is ~10x the cost).
@@ -964,17 +978,26 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   };
   const int64_t wa = owner(pb);
   const int64_t wb = owner(pb + pn - 1);
-  if (wa == wb) return;  // one range held all of it and wrote the output
+  const bool whole = wa == wb;
+  if (whole && !cascade) return;  // one range held all of it and wrote the output
   const int s_first = start(wa) < pb ? 1 : 0;
-  const int n = static_cast<int>(wb - wa + 1);
+  // Items: pass 1's pieces (a whole sequence of a cascaded call: its one partial
+  // row at prefix split pre_splits), then the prefix splits that hold shared keys.
+  const int n_s = whole ? 1 : static_cast<int>(wb - wa + 1);
+  const int n_p = cascade ? min(p.pre_splits, (*p.shared_blocks * p.block_size + p.split_keys - 1) / p.split_keys)
+                          : 0;
+  const int n = n_s + n_p;
+  auto pre_row = [&](int sp) -> int64_t {
+    return p.pre_row0 + (static_cast<int64_t>(sp) * p.batch + b) * p.num_heads + h;
+  };
   auto row = [&](int i) -> int64_t {
+    if (i >= n_s) return pre_row(i - n_s);
+    if (whole) return pre_row(p.pre_splits);
     return (((wa + i) * p.num_kv_heads + kh) * 2 + (i == 0 ? s_first : 0)) * G + q;
   };
   // Pieces of empty ranges (fewer keys than ranges) were never written.
-  auto piece_lse = [&](int i) -> float {
-    const int64_t v = wa + i;
-    return start(v) < start(v + 1) ? p.part_lse[row(i)] : -INFINITY;
-  };
+  auto item_valid = [&](int i) -> bool { return i >= n_s || whole || start(wa + i) < start(wa + i + 1); };
+  auto piece_lse = [&](int i) -> float { return item_valid(i) ? p.part_lse[row(i)] : -INFINITY; };
   // One round of loads for the common case: lane l's piece log2-sum-exp and
   // the partial rows of the first eight pieces are issued together (clamped
   // indices, weights 0 select the extra ones away).
@@ -987,7 +1010,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
 #pragma unroll
     for (int k = 0; k < PER; ++k) pv0[j][k] = po[64 * k];
   }
-  const float lse_l = lane < n && start(wa + lane) < start(wa + lane + 1) ? lse0 : -INFINITY;
+  const float lse_l = lane < n && item_valid(lane) ? lse0 : -INFINITY;
   float M = lse_l;
   for (int i = lane + 64; i < n; i += 64) M = fmaxf(M, piece_lse(i));  // more than 64 pieces
 #pragma unroll
@@ -1325,6 +1348,51 @@ extern "C" int64_t paged_decode_attention_path_split_tokens(int path, int64_t ba
   }
 }
 
+namespace {
+// Workspace of a cascaded call: the stream pass's partial rows, then the prefix
+// rows ((splits + 1) per query row: the prefix splits, then the whole-sequence
+// partials of the stream pass), their log2-sum-exps, the attended-key prefix
+// sums, and the number of shared blocks the prefix pass found.
+struct CascadeLayout {
+  int64_t stream_rows, lse_off, cu_off, shared_off, total;
+  int splits, split_keys;
+};
+constexpr int kPrefixSplitKeys = 512;  // keys per prefix split (a multiple of the prefill tile)
+CascadeLayout cascade_layout(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+                             int64_t page_block_size, int64_t shared_hint) {
+  CascadeLayout c;
+  int wgs = device_cu_count();
+  wgs -= wgs % kXcds;
+  c.stream_rows = 2 * static_cast<int64_t>(wgs) * (kStreamWaves / num_kv_heads) * num_heads;
+  // Splits of 512 keys, halved while the prefix pass would fill fewer than ~2 workgroups per CU.
+  const int64_t keys = std::max<int64_t>(shared_hint, 1) * page_block_size;
+  const int64_t row_tiles = ceil_div(batch * (num_heads / num_kv_heads), 128);
+  c.split_keys = kPrefixSplitKeys;
+  while (c.split_keys > 64 && ceil_div(keys, c.split_keys) * num_kv_heads * row_tiles < 2 * wgs) c.split_keys /= 2;
+  c.splits = static_cast<int>(ceil_div(keys, c.split_keys));
+  const int64_t rows = c.stream_rows + (c.splits + 1) * batch * num_heads;
+  const WorkspaceLayout wl = workspace_layout(rows, head_dim);
+  c.lse_off = wl.lse_off;
+  c.cu_off = ceil_div(wl.total, 256) * 256;
+  c.shared_off = c.cu_off + ceil_div((batch + 1) * 4, 256) * 256;
+  c.total = c.shared_off + 256;
+  return c;
+}
+}  // namespace
+
+extern "C" size_t paged_decode_attention_shared_prefix_workspace_size(int64_t batch, int64_t num_heads,
+                                                                     int64_t num_kv_heads, int64_t head_dim,
+                                                                     int64_t page_block_size, int64_t max_seqlen_k,
+                                                                     int64_t shared_blocks_hint) {
+  const size_t plain = paged_decode_attention_workspace_size(batch, num_heads, num_kv_heads, head_dim, max_seqlen_k);
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0 ||
+      page_block_size <= 0 || shared_blocks_hint <= 0 || num_heads % num_kv_heads != 0)
+    return plain;
+  const CascadeLayout c = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                                         std::min(shared_blocks_hint, ceil_div(max_seqlen_k, page_block_size)));
+  return std::max(plain, static_cast<size_t>(c.total));
+}
+
 extern "C" int64_t paged_decode_attention_pass1(int path, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
                                                 int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k) {
   const bool rows_ok = oxide::rows_path_ok(batch, num_heads, num_kv_heads, head_dim, page_block_size);
@@ -1365,7 +1433,7 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
                            int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
                            int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left,
                            float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
-                           void* stream) {
+                           void* stream, int64_t shared_hint = 0) {
   if (dtype != OXIDE_DTYPE_BF16 && dtype != OXIDE_DTYPE_F16) {
     oxide::set_error(OXIDE_ERR_UNSUPPORTED_DTYPE);
     return;
@@ -1387,6 +1455,83 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
   if ((head_dim != 64 && head_dim != 128) || page_block_size % 16 != 0 ||
       group < 1 || (group > 8 && group != 16)) {
     oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
+    return;
+  }
+  if (shared_hint > 0 && max_seqlen_k > 0 && stream_ok(batch, num_kv_heads) && (group <= 8 || group == 16)) {
+    // Cascaded call: the shared prefix on the matrix cores once for the whole batch,
+    // the rest by the stream pass, both merged by the stream merge.
+    // Never more shared blocks than the longest sequence has (the size query clamps alike).
+    shared_hint = std::min(shared_hint, ceil_div(max_seqlen_k, page_block_size));
+    const CascadeLayout cl = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, shared_hint);
+    if (workspace_bytes < static_cast<size_t>(cl.total) || !workspace) {
+      oxide::set_error(OXIDE_ERR_WORKSPACE_TOO_SMALL);
+      return;
+    }
+    char* ws = static_cast<char*>(workspace);
+    DecodeParams p{};
+    p.q = q;
+    p.k = k_cache;
+    p.v = v_cache;
+    p.cu_seqlens_k = cu_seqlens_k;
+    p.block_table = block_table;
+    p.part_o = reinterpret_cast<float*>(ws);
+    p.part_lse = reinterpret_cast<float*>(ws + cl.lse_off);
+    p.attn_cu = reinterpret_cast<uint32_t*>(ws + cl.cu_off);
+    p.shared_blocks = reinterpret_cast<const int*>(ws + cl.shared_off);
+    p.pre_row0 = cl.stream_rows;
+    p.pre_splits = cl.splits;
+    p.split_keys = cl.split_keys;
+    p.whole_row0 = cl.stream_rows + static_cast<int64_t>(cl.splits) * batch * num_heads;
+    p.out = out;
+    p.new_k = new_k;
+    p.new_v = new_v;
+    p.slot_mapping = slot_mapping;
+    p.max_blocks = max_blocks_per_seq;
+    p.num_blocks = static_cast<int>(num_blocks);
+    p.max_seqlen_k = static_cast<int>(max_seqlen_k);
+    p.num_heads = static_cast<int>(num_heads);
+    p.num_kv_heads = static_cast<int>(num_kv_heads);
+    p.block_size = static_cast<int>(page_block_size);
+    p.window_left = window_left < 0 ? -1 : window_left;
+    p.split_tokens = -1;  // the stream pass
+    p.stream_deep = 1;    // its ranges over the private keys are short
+    p.max_splits = 1;
+    p.batch = static_cast<int>(batch);
+    p.scale_log2 = softmax_scale * 1.4426950408889634f;
+    hipStream_t s = oxide::as_stream(stream);
+    oxide::DecodePrefixArgs a{};
+    a.q = q;
+    a.k = k_cache;
+    a.v = v_cache;
+    a.cu_seqlens_k = cu_seqlens_k;
+    a.block_table = block_table;
+    a.max_blocks = max_blocks_per_seq;
+    a.num_blocks = static_cast<int>(num_blocks);
+    a.batch = static_cast<int>(batch);
+    a.num_heads = static_cast<int>(num_heads);
+    a.num_kv_heads = static_cast<int>(num_kv_heads);
+    a.head_dim = static_cast<int>(head_dim);
+    a.block_size = static_cast<int>(page_block_size);
+    a.max_seqlen_k = static_cast<int>(max_seqlen_k);
+    a.window_left = p.window_left;
+    a.scale_log2 = p.scale_log2;
+    a.part_o = p.part_o;
+    a.part_lse = p.part_lse;
+    a.pre_row0 = cl.stream_rows;
+    a.pre_splits = cl.splits;
+    a.split_keys = cl.split_keys;
+    a.shared_hint = static_cast<int>(shared_hint);
+    a.shared_out = reinterpret_cast<int*>(ws + cl.shared_off);
+    a.bf16 = dtype == OXIDE_DTYPE_BF16;
+    const bool ok = oxide::launch_decode_prefix(a, s) &&
+                    (dtype == OXIDE_DTYPE_BF16
+                         ? dispatch<Bf16Tag>(p, batch, static_cast<int>(head_dim), static_cast<int>(group), s)
+                         : dispatch<F16Tag>(p, batch, static_cast<int>(head_dim), static_cast<int>(group), s));
+    if (!ok) {
+      oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
+      return;
+    }
+    oxide::check_launch();
     return;
   }
   const bool rows_ok = oxide::rows_path_ok(batch, num_heads, num_kv_heads, head_dim, page_block_size);
@@ -1412,6 +1557,7 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
     return;
   }
   DecodeParams p{};
+  p.whole_row0 = -1;  // no cascade
   p.q = q;
   p.k = k_cache;
   p.v = v_cache;
@@ -1472,7 +1618,7 @@ void decode_append_impl(bool compact_ws, int forced_path, void* out, const void*
                         const int32_t* block_table, int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
                         int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
                         int64_t max_seqlen_k, int32_t window_left, float softmax_scale, void* workspace,
-                        size_t workspace_bytes, int dtype, void* stream) {
+                        size_t workspace_bytes, int dtype, void* stream, int64_t shared_hint = 0) {
   if (batch > 0 && (!key || !value || !slot_mapping || !oxide::aligned16(key) ||
                     !oxide::aligned16(value))) {
     oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
@@ -1491,7 +1637,7 @@ void decode_append_impl(bool compact_ws, int forced_path, void* out, const void*
   decode_attention_impl(compact_ws, forced_path, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k,
                         block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
                         num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
-                        softmax_scale, workspace, workspace_bytes, dtype, stream);
+                        softmax_scale, workspace, workspace_bytes, dtype, stream, shared_hint);
 }
 }  // namespace
 
@@ -1505,6 +1651,29 @@ extern "C" void paged_decode_attention_append(
   decode_append_impl(false, 0, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
                      max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
                      max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream);
+}
+
+extern "C" void paged_decode_attention_shared_prefix(
+    void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping, void* k_cache,
+    void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table, int64_t max_blocks_per_seq,
+    int64_t num_blocks, int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
+    int64_t shared_blocks_hint, void* workspace, size_t workspace_bytes, int dtype, void* stream) {
+  if (shared_blocks_hint < 0) {
+    oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
+    return;
+  }
+  if (key == nullptr && value == nullptr && slot_mapping == nullptr) {
+    decode_attention_impl(false, 0, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k, block_table,
+                          max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                          max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream,
+                          shared_blocks_hint);
+    return;
+  }
+  decode_append_impl(false, 0, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
+                     max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
+                     max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream,
+                     shared_blocks_hint);
 }
 
 extern "C" void paged_decode_attention_path(

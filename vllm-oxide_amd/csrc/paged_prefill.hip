@@ -44,6 +44,7 @@
 #include <type_traits>
 
 #include "cdna4_tile.hpp"
+#include "decode_common.hpp"
 #include "oxide_common.hpp"
 
 namespace {
@@ -76,10 +77,50 @@ struct PrefillParams {
   int block_size;
   int window_left;
   float scale_log2;
+  // Shared-prefix pass of a decode batch (kernel instances with kPrefix): the rows
+  // are the decode batch's (sequence, query head) pairs -- q [dec_batch, Hq, D],
+  // cu_seqlens_k the decode batch's -- and the keys are the leading block-table
+  // entries that every row shares (at most shared_hint of them; the kernel finds
+  // how many), cut into pre_splits splits of split_keys keys.  Each (split,
+  // sequence, head) writes a normalised partial row and its log2-sum-exp at row
+  // pre_row0 + split * dec_batch * Hq + b * Hq + h of part_o / part_lse.
+  float* part_o;
+  float* part_lse;
+  int64_t pre_row0;
+  int pre_splits;
+  int split_keys;
+  int shared_hint;
+  int dec_batch;
+  int* shared_out;  // the number of shared blocks found (written by workgroup 0)
 };
 
 __device__ __forceinline__ int clamp_len(int64_t n, int cap) {
   return static_cast<int>(n < 0 ? 0 : (n > cap ? cap : n));
+}
+
+// Shared-prefix pass: the number of leading block-table entries identical in every
+// row of the decode batch, at most shared_hint, and at most (L_b - 1) / block_size
+// for every sequence b (so each sequence keeps at least its newest key outside the
+// prefix; an empty sequence makes it 0).  Every workgroup computes it the same way
+// (a scan of batch x shared_hint table entries, cooperative, through LDS minima).
+__device__ __forceinline__ int shared_prefix_blocks(const PrefillParams& p) {
+  __shared__ int s_blocks;
+  if (threadIdx.x == 0) s_blocks = p.shared_hint;
+  __syncthreads();
+  for (int b = threadIdx.x; b < p.dec_batch; b += kPfThreads) {
+    const int L = clamp_len(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - p.cu_seqlens_k[b], p.max_seqlen_k);
+    atomicMin(&s_blocks, L > 0 ? (L - 1) / p.block_size : 0);
+  }
+  __syncthreads();
+  const int n0 = s_blocks;
+  const int64_t total = static_cast<int64_t>(p.dec_batch - 1) * n0;
+  for (int64_t x = threadIdx.x; x < total; x += kPfThreads) {
+    const int64_t b = 1 + x / n0;
+    const int jj = static_cast<int>(x % n0);
+    if (p.block_table[b * p.max_blocks + jj] != p.block_table[jj]) atomicMin(&s_blocks, jj);
+  }
+  __syncthreads();
+  return s_blocks;
 }
 
 // LDS tile layouts (64 keys, row = one key's head slice of 2*D bytes):
@@ -131,7 +172,7 @@ enum PrefillAddressing {
   kPagedRows = 2,   // paged, any block_size: a block lookup per row
 };
 
-template <class Tag, int D, int MODE>
+template <class Tag, int D, int MODE, bool kPrefix>
 __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParams p) {
   constexpr int CH = D / 8;                  // 16-byte chunks per head row
   constexpr int KS = D / 16;                 // MFMA k-steps of Q.K (16 dims each)
@@ -150,17 +191,28 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   __shared__ __align__(1024) char smem1[BUF];
 
   // XCD-aware work item: unit (sequence, kv head) u sits on XCD u % 8 and its
-  // tiles are consecutive workgroups there, heaviest first.
+  // tiles are consecutive workgroups there, heaviest first.  Shared-prefix pass:
+  // unit (key split, kv head), all of them over table row 0 (the shared entries).
   const int i = blockIdx.x;
   const int j = i / kPfXcds;
   const int u = (j / p.tiles_per_unit) * kPfXcds + i % kPfXcds;
   if (u >= p.units) return;
   const int tile = p.tiles_per_unit - 1 - j % p.tiles_per_unit;
-  const int b = u / p.num_kv_heads;
+  const int b = kPrefix ? 0 : u / p.num_kv_heads;
   const int kh = u % p.num_kv_heads;
+  const int split = kPrefix ? u / p.num_kv_heads : 0;
 
-  const int Lq = clamp_len(static_cast<int64_t>(p.cu_seqlens_q[b + 1]) - p.cu_seqlens_q[b], p.max_seqlen_q);
-  const int Lk = clamp_len(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - p.cu_seqlens_k[b], p.max_seqlen_k);
+  int Lq, Lk;
+  if constexpr (kPrefix) {
+    const int shared = shared_prefix_blocks(p);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *p.shared_out = shared;
+    Lq = p.dec_batch;
+    Lk = shared * p.block_size;  // the shared keys; no sequence attends past them here
+    if (split * p.split_keys >= Lk) return;
+  } else {
+    Lq = clamp_len(static_cast<int64_t>(p.cu_seqlens_q[b + 1]) - p.cu_seqlens_q[b], p.max_seqlen_q);
+    Lk = clamp_len(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - p.cu_seqlens_k[b], p.max_seqlen_k);
+  }
   const int t0 = tile * p.tokens_per_wg;
   if (t0 >= Lq) return;
   const int t1 = min(Lq, t0 + p.tokens_per_wg);
@@ -168,15 +220,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   const int G = p.group;
   const int W = p.window_left;
 
-  // Key range of the workgroup: [klo, khi] (empty when khi < klo).
-  const int khi = min(Lk - 1, t1 - 1 + off);
-  const int klo = W >= 0 ? max(0, t0 + off - W) : 0;
+  // Key range of the workgroup: [klo, khi] (empty when khi < klo).  Shared-prefix
+  // pass: the split's keys, every row seeing all of them but those before its window.
+  const int khi = kPrefix ? min(Lk, (split + 1) * p.split_keys) - 1 : min(Lk - 1, t1 - 1 + off);
+  const int klo = kPrefix ? split * p.split_keys : (W >= 0 ? max(0, t0 + off - W) : 0);
   const int kt0 = klo & ~(kPfKeys - 1);
   const int ntiles = khi >= klo ? (khi - kt0) / kPfKeys + 1 : 0;
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int64_t q0 = p.cu_seqlens_q[b];
+  const int64_t q0 = kPrefix ? 0 : p.cu_seqlens_q[b];
   const int rows_used = p.tokens_per_wg * G;
 
   // This lane's row (column l % 32 of the MFMA tiles; lanes l and l + 32 share
@@ -187,15 +240,24 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   const int tq = t0 + rr / G;
   const bool valid = rr < rows_used && tq < t1;
   const int64_t qrow = valid ? (q0 + tq) * p.num_heads + kh * G + rr % G : 0;
-  const int hi_r = valid ? tq + off : -1;
-  const int lo_r = valid && W >= 0 ? tq + off - W : 0;
+  int hi_r = valid ? tq + off : -1;
+  int lo_r = valid && W >= 0 ? tq + off - W : 0;
+  if constexpr (kPrefix) {
+    // Decode sequence tq attends keys [max(0, L - 1 - W), L) of which the shared
+    // ones are [.., Lk); this split holds [klo, khi].
+    const int L = valid ? clamp_len(static_cast<int64_t>(p.cu_seqlens_k[tq + 1]) - p.cu_seqlens_k[tq],
+                                    p.max_seqlen_k)
+                        : 0;
+    hi_r = valid ? khi : -1;
+    lo_r = valid && W >= 0 ? L - 1 - W : 0;
+  }
   // Key range of the wave's valid rows (wave-uniform) for skipping tiles.
   const int wr0 = wave * 32;
   const int wt_first = t0 + wr0 / G;
   const int wt_last = min(t1 - 1, t0 + min(wr0 + 31, rows_used - 1) / G);
   const bool wave_active = wr0 < rows_used && wt_first < t1;
-  const int wave_hi = min(Lk - 1, wt_last + off);
-  const int wave_lo = W >= 0 ? wt_first + off - W : 0;
+  const int wave_hi = kPrefix ? khi : min(Lk - 1, wt_last + off);
+  const int wave_lo = kPrefix ? 0 : (W >= 0 ? wt_first + off - W : 0);
 
   // Queries (B operand of S^T, 16 dims per k-step).  A negative scale is
   // applied as a sign flip of q (exact) and |scale|, so the running maxima can
@@ -427,7 +489,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   // out[row][d] for d = 32 db + 8 q + 4 half + e (register 4 q + e), normalised
   // by the row total (both halves of the keys).
   lsum = sum_over_halves(lsum);
-  if (valid) {
+  if (kPrefix && valid) {
+    // Normalised partial row and its log2-sum-exp (scores are in units of
+    // |scale| log2 e, as the decode passes' partials).
+    const float l = lsum;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int64_t prow = p.pre_row0 + static_cast<int64_t>(split) * p.dec_batch * p.num_heads + qrow;
+    float* po = p.part_o + prow * D + 4 * half;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<float4*>(po + 32 * db + 8 * q) =
+            make_float4(acc[db][4 * q + 0] * inv, acc[db][4 * q + 1] * inv, acc[db][4 * q + 2] * inv,
+                        acc[db][4 * q + 3] * inv);
+    if (half == 0) p.part_lse[prow] = l > 0.f ? m_r + log2f(l) : -INFINITY;
+  } else if (valid) {
     const float l = lsum;
     const float inv = l > 0.f ? 1.f / l : 0.f;
     uint16_t* op = static_cast<uint16_t*>(p.out) + qrow * D + 4 * half;
@@ -448,11 +525,19 @@ int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 template <class Tag, int D>
 void launch_mode(const PrefillParams& p, dim3 grid, hipStream_t s) {
   if (p.block_table == nullptr)
-    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kContiguous>), grid, dim3(kPfThreads), 0, s, p);
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kContiguous, false>), grid, dim3(kPfThreads), 0, s, p);
   else if (p.block_size % kPfKeys == 0)
-    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedTiles>), grid, dim3(kPfThreads), 0, s, p);
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedTiles, false>), grid, dim3(kPfThreads), 0, s, p);
   else
-    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedRows>), grid, dim3(kPfThreads), 0, s, p);
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedRows, false>), grid, dim3(kPfThreads), 0, s, p);
+}
+
+template <class Tag, int D>
+void launch_prefix_mode(const PrefillParams& p, dim3 grid, hipStream_t s) {
+  if (p.block_size % kPfKeys == 0)
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedTiles, true>), grid, dim3(kPfThreads), 0, s, p);
+  else
+    hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedRows, true>), grid, dim3(kPfThreads), 0, s, p);
 }
 
 template <class Tag>
@@ -579,3 +664,48 @@ extern "C" void varlen_prefill_attention(void* out, const void* q, const void* k
                num_kv_heads, head_dim, 1, max_seqlen_q, max_seqlen_k, window_left, softmax_scale,
                dtype, stream);
 }
+
+namespace oxide {
+
+// Shared-prefix pass of a cascaded decode call (declared in decode_common.hpp).
+bool launch_decode_prefix(const DecodePrefixArgs& a, hipStream_t s) {
+  PrefillParams p{};
+  p.q = a.q;
+  p.k = a.k;
+  p.v = a.v;
+  p.cu_seqlens_k = a.cu_seqlens_k;
+  p.block_table = a.block_table;
+  p.max_blocks = a.max_blocks;
+  p.num_blocks = a.num_blocks;
+  p.num_rows = static_cast<int64_t>(a.num_blocks) * a.block_size;
+  p.max_seqlen_k = a.max_seqlen_k;
+  p.num_heads = a.num_heads;
+  p.num_kv_heads = a.num_kv_heads;
+  p.group = a.num_heads / a.num_kv_heads;
+  p.tokens_per_wg = kPfRows / p.group;
+  p.tiles_per_unit = static_cast<int>(ceil_div64(a.batch, p.tokens_per_wg));
+  p.units = a.num_kv_heads * a.pre_splits;
+  p.block_size = a.block_size;
+  p.window_left = a.window_left < 0 ? -1 : a.window_left;
+  p.scale_log2 = a.scale_log2;
+  p.part_o = a.part_o;
+  p.part_lse = a.part_lse;
+  p.pre_row0 = a.pre_row0;
+  p.pre_splits = a.pre_splits;
+  p.split_keys = a.split_keys;
+  p.shared_hint = a.shared_hint;
+  p.dec_batch = a.batch;
+  p.shared_out = a.shared_out;
+  const dim3 grid(static_cast<unsigned>(ceil_div64(p.units, kPfXcds) * kPfXcds * p.tiles_per_unit));
+  if (a.head_dim == 128) {
+    a.bf16 ? launch_prefix_mode<Bf16Tag, 128>(p, grid, s) : launch_prefix_mode<F16Tag, 128>(p, grid, s);
+    return true;
+  }
+  if (a.head_dim == 64) {
+    a.bf16 ? launch_prefix_mode<Bf16Tag, 64>(p, grid, s) : launch_prefix_mode<F16Tag, 64>(p, grid, s);
+    return true;
+  }
+  return false;
+}
+
+}  // namespace oxide

@@ -32,6 +32,11 @@ SIGNATURES = {
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
         ctypes.c_int32, ctypes.c_float, ctypes.c_int, _p]),
     "paged_decode_attention_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64]),
+    "paged_decode_attention_shared_prefix": (None, [
+        _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        ctypes.c_int32, ctypes.c_float, _i64, _p, ctypes.c_size_t, ctypes.c_int, _p]),
+    "paged_decode_attention_shared_prefix_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, _i64,
+                                                                              _i64]),
     "paged_decode_attention_split_tokens": (_i64, [_i64, _i64, _i64]),
     "paged_decode_attention_path_split_tokens": (_i64, [ctypes.c_int, _i64, _i64, _i64]),
     "paged_decode_attention_pass1": (_i64, [ctypes.c_int, _i64, _i64, _i64, _i64, _i64, _i64]),

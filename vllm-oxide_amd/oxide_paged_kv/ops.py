@@ -121,7 +121,7 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 softmax_scale: float, window_left: int | None = None,
                 page_block_size: int = 256, out: torch.Tensor | None = None,
                 workspace: torch.Tensor | None = None, append=None, path: int | str = 0,
-                noalloc: bool = False) -> torch.Tensor:
+                noalloc: bool = False, shared_prefix_blocks: int | None = None) -> torch.Tensor:
     """Paged decode attention.
 
     q [B, Hq, D]; k_cache/v_cache [NB, page_block_size, Hkv, D]; cu_seqlens_k uint32-valued
@@ -133,6 +133,9 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     through paged_decode_attention_path for this call only.
     noalloc: call paged_decode_attention_noalloc (partials in the library's static device
     scratch; no workspace is allocated or passed; path must be "auto").
+    shared_prefix_blocks: an upper bound on the leading block-table entries every row
+    shares -> paged_decode_attention_shared_prefix (the shared keys attended once for the
+    whole batch; the library finds the actual count); path must be "auto".
     """
     L = _lib.load()
     B, Hq, D = q.shape
@@ -159,6 +162,20 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         L.paged_decode_attention_noalloc(_ptr(out), _ptr(q), *kv, _ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k),
                                          _ptr(block_table), max_blocks, NB, B, Hq, Hkv, D, BS, max_seqlen_k, w,
                                          float(softmax_scale), dtype_code(q.dtype), _stream(q))
+        _lib.check()
+        return out
+    if shared_prefix_blocks is not None:
+        if path != 0 or noalloc:
+            raise _lib.OxideError("shared_prefix_blocks takes no forced path and no noalloc")
+        need = int(L.paged_decode_attention_shared_prefix_workspace_size(B, Hq, Hkv, D, BS, max_seqlen_k,
+                                                                         int(shared_prefix_blocks)))
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
+        kv = (None, None, None) if append is None else (_ptr(key), _ptr(value), _ptr(slot_mapping))
+        L.paged_decode_attention_shared_prefix(
+            _ptr(out), _ptr(q), *kv, _ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k), _ptr(block_table), max_blocks,
+            NB, B, Hq, Hkv, D, BS, max_seqlen_k, w, float(softmax_scale), int(shared_prefix_blocks), _ptr(workspace),
+            workspace.numel() * workspace.element_size(), dtype_code(q.dtype), _stream(q))
         _lib.check()
         return out
     need = workspace_size(B, Hq, Hkv, D, max_seqlen_k)
