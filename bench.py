@@ -19,7 +19,9 @@ Prints ONE JSON line.  value = algorithmic bytes of (append + attention) per
 step / wall time per step.  The attention call (pass-1 kernel + LSE merge
 kernel) is also timed with HIP events on the stream it runs on: two events
 bracketing the timed steps (one call per step in the default fused mode) ->
-attn_us and roofline.
+attn_us and roofline.  Where sequences share cache blocks (configuration 4's
+prefix) the call is the cascaded entry and the algorithmic bytes count each
+distinct cache row once; the per-sequence count is reported beside them.
 The step's K/V/q bytes come from a seeded host generator and are uploaded, so
 cpu_baseline -- the C oracle (test infrastructure, reference semantics) over
 the whole step on the same bytes -- also checks the GPU step's output
@@ -489,34 +491,56 @@ def measure_config(cfg_id: int, dev, seed: int, steps: int = 100, warmup: int = 
         res["cow_copy_blocks_us"] = round(cow_us, 2)
         res["cow_copy_blocks_gbps"] = round(cow_bytes / (cow_us * 1e-6) / 1e9, 1)
 
-    def call(i):
+    # A batch whose block tables share a prefix (cfg4) runs the cascaded entry: the
+    # shared blocks attended once for all sequences (the hint is an upper bound; the
+    # library finds the shared count on the device).  The plain call is timed too.
+    hint = cfg.shared_prefix // cfg.block_size if cfg.shared_prefix else None
+    if hint:
+        ws = torch.empty(ox.shared_prefix_workspace_size(cfg.batch, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim,
+                                                         cfg.block_size, st.max_seqlen_k, hint),
+                         dtype=torch.uint8, device=dev)
+
+    def call(i, cascade=True):
         layer = i % layers
         ox.decode_attn(q[layer], buf[0, layer], buf[1, layer], cu, bt, st.max_seqlen_k, scale, window,
-                       cfg.block_size, out=out, workspace=ws, append=(knew[layer], vnew[layer], sm))
+                       cfg.block_size, out=out, workspace=ws, append=(knew[layer], vnew[layer], sm),
+                       shared_prefix_blocks=hint if cascade else None)
 
-    for i in range(warmup):
-        call(i)
-    torch.cuda.synchronize()
-    # A few ms of device work ahead of the bracket (a fill of a 4 GiB buffer, twice), so
-    # the host has enqueued the timed calls before the GPU reaches them: for calls shorter
-    # than their Python launch cost (cfg1) the bracket then times the device, not the host.
-    filler = torch.empty(1 << 31, dtype=torch.int16, device=dev)
-    filler.fill_(1)
-    filler.fill_(2)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(steps):
-        call(warmup + i)
-    e1.record()
-    torch.cuda.synchronize()
-    del filler
-    us = e0.elapsed_time(e1) / steps * 1e3
-    nbytes = st.attn_bytes() + st.append_bytes()
+    def timed(cascade=True):
+        for i in range(warmup):
+            call(i, cascade)
+        torch.cuda.synchronize()
+        # A few ms of device work ahead of the bracket (a fill of a 4 GiB buffer, twice), so
+        # the host has enqueued the timed calls before the GPU reaches them: for calls shorter
+        # than their Python launch cost (cfg1) the bracket then times the device, not the host.
+        filler = torch.empty(1 << 31, dtype=torch.int16, device=dev)
+        filler.fill_(1)
+        filler.fill_(2)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(steps):
+            call(warmup + i, cascade)
+        e1.record()
+        torch.cuda.synchronize()
+        del filler
+        return e0.elapsed_time(e1) / steps * 1e3
+
+    if hint:
+        plain_us = timed(cascade=False)
+        res["no_cascade_attn_us"] = round(plain_us, 2)
+    us = timed()
+    # With shared blocks the algorithmic bytes count each distinct cache row once (the
+    # least a call that reads a shared row once must move); the bytes a per-sequence
+    # read would move (the reference's) are reported beside them.
+    ref_bytes = st.attn_bytes() + st.append_bytes()
+    nbytes = st.attn_unique_bytes() + st.append_bytes()
     gbps = nbytes / (us * 1e-6) / 1e9
     split = ox.split_tokens(cfg.batch, cfg.num_kv_heads, st.max_seqlen_k, num_heads=cfg.num_heads,
                             head_dim=cfg.head_dim, page_block_size=cfg.block_size)
     traffic = profiled_traffic(cfg_id, False)
-    res.update({"workload": cfg.name, "pass1": PASS1_NAMES[_pass1(split)], "attn_us": round(us, 2),
+    pass1 = PASS1_NAMES[_pass1(split)] if not hint else \
+        "cascade: shared-prefix pass (paged_prefill_attn prefix mode) + wave-level stream over the rest"
+    res.update({"workload": cfg.name, "pass1": pass1, "attn_us": round(us, 2),
                 "algorithmic_bytes": nbytes, "attn_gbps": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
                 "traffic": traffic, "tokens_per_s": round(cfg.batch / (us * 1e-6), 1),
                 "calls": steps, "layers_rotated": layers})
@@ -524,9 +548,9 @@ def measure_config(cfg_id: int, dev, seed: int, steps: int = 100, warmup: int = 
         # HBM bytes the call actually moves (rocprofv3 FETCH_SIZE + WRITE_SIZE summary
         # under profiles/) over the same time.
         res["hbm_frac"] = round(traffic / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)
-        if traffic < 0.9 * nbytes:
-            res["frac_note"] = ("the algorithmic bytes include re-reads served from L2 (the shared "
-                                "prefix): hbm_frac, over the HBM bytes moved, is the roofline figure")
+    if ref_bytes != nbytes:
+        res["reference_equivalent_bytes"] = ref_bytes
+        res["reference_equivalent_gbps"] = round(ref_bytes / (us * 1e-6) / 1e9, 1)
     if cfg.layers > 1:
         res["step_us_all_layers"] = round(us * cfg.layers, 1)
     del buf
@@ -576,6 +600,11 @@ def decode_main(args) -> int:
         pairs = torch.from_numpy(st.cow_pairs).to(dev)
         for layer in range(layers):
             ox.copy_blocks(buf[0, layer], buf[1, layer], pairs)
+    # A batch sharing a block-table prefix (cfg4) takes the cascaded entry in the fused mode.
+    hint = cfg.shared_prefix // BS if cfg.shared_prefix and not args.separate and args.path == "auto" else None
+    if hint:
+        ws = torch.zeros(ox.shared_prefix_workspace_size(cfg.batch, cfg.num_heads, H, D, BS, st.max_seqlen_k, hint),
+                         dtype=torch.uint8, device=dev)
 
     def step(i, ev=None):
         layer = i % layers
@@ -591,7 +620,7 @@ def decode_main(args) -> int:
             if ev:
                 ev[1].record()
             ox.decode_attn(q, kc, vc, cu, bt, st.max_seqlen_k, scale, window, BS, out=out,
-                           workspace=ws, append=(knew, vnew, sm), path=path)
+                           workspace=ws, append=(knew, vnew, sm), path=path, shared_prefix_blocks=hint)
         if ev:
             ev[2].record()
 
@@ -635,7 +664,9 @@ def decode_main(args) -> int:
     gpu_out = out.float().cpu().numpy()  # the last step's output (every layer holds the same inputs)
     att_ms = [e[1].elapsed_time(e[2]) for e in evs]
     ms_per_step = wall * 1e3 / args.steps
-    attn_bytes, app_bytes = st.attn_bytes(), st.append_bytes()
+    # Shared blocks (the cascade): each distinct cache row counts once, as in measure_config.
+    attn_bytes, app_bytes = (st.attn_unique_bytes() if hint else st.attn_bytes()), st.append_bytes()
+    kv_bytes = st.unique_kv_read_bytes() if hint else st.kv_read_bytes()
     # Fused: the bracketed average.  Separate (append + attention per step): the
     # attention call's own events from the second pass.
     attn_us = float(np.mean(att_ms)) * 1e3 if args.separate else bracket_us
@@ -741,7 +772,7 @@ def decode_main(args) -> int:
         # overhead lengthens each call by a few us).
         "attn_us_per_call_events_p10_p50_p90": [round(float(np.percentile(att_ms, q)) * 1e3, 2)
                                                 for q in (10, 50, 90)],
-        "attn_kv_read_gbps": round(st.kv_read_bytes() / (attn_us * 1e-6) / 1e9, 1),
+        "attn_kv_read_gbps": round(kv_bytes / (attn_us * 1e-6) / 1e9, 1),
         "attn_gbps": round(attn_gbps, 1),
         "attn_hbm_frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
         "append_us": round(app_us, 2),
@@ -750,11 +781,16 @@ def decode_main(args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": profiled_traffic(args.config, args.separate) if args.path == "auto" else None,
-                     "kernel": PASS1_KERNELS[_pass1(split)]
+                     "kernel": ("paged_prefill_attn (shared-prefix mode) + " if hint else "")
+                               + PASS1_KERNELS[_pass1(split)]
                                + " (one attention call" + ("" if args.separate else ", append fused") + ")",
                      "algorithmic_bytes": call_bytes},
         **extra,
     }
+    if hint:
+        ref_bytes = st.attn_bytes() + (0 if args.separate else app_bytes)
+        res["reference_equivalent_bytes"] = ref_bytes
+        res["reference_equivalent_gbps"] = round(ref_bytes / (attn_us * 1e-6) / 1e9, 1)
     if not args.no_cpu_baseline:
         threads = min(16, os.cpu_count() or 1)
         res["cpu_baseline"], cpu_out = cpu_baseline(st, h, threads)

@@ -912,7 +912,9 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(Decode
 // per piece reads its log2-sum-exp, the weights are reduced across the wave,
 // and each lane then accumulates D / 64 output dims over the pieces, so the
 // whole merge is three dependent rounds of loads (lengths, lse, partials).
-template <class Tag, int D>
+// kChunk: pieces whose partial rows are loaded per round (16 for cascaded calls,
+// whose (sequence, head) rows also gather the prefix splits).
+template <class Tag, int D, int kChunk = 8>
 __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) {
   constexpr int PER = D / 64;
   const int h = blockIdx.x;
@@ -1003,9 +1005,9 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   // indices, weights 0 select the extra ones away).
   const int il = min(lane, n - 1);
   const float lse0 = p.part_lse[row(il)];
-  float pv0[8][PER];
+  float pv0[kChunk][PER];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
+  for (int j = 0; j < kChunk; ++j) {
     const float* po = p.part_o + row(min(j, n - 1)) * D + lane;
 #pragma unroll
     for (int k = 0; k < PER; ++k) pv0[j][k] = po[64 * k];
@@ -1032,10 +1034,10 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
     // first eight were loaded above).  A piece with weight 0 (an empty range:
     // its row was never written, or one wholly left of the window) is
     // selected away, not multiplied.
-    for (int i0 = 0; i0 < cnt; i0 += 8) {
-      float wv[8], pv[8][PER];
+    for (int i0 = 0; i0 < cnt; i0 += kChunk) {
+      float wv[kChunk], pv[kChunk][PER];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
+      for (int j = 0; j < kChunk; ++j) {
         const int i = i0 + j;
         wv[j] = i < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i)) : 0.f;
         if (g == 0 && i0 == 0) {
@@ -1048,7 +1050,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
         }
       }
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
+      for (int j = 0; j < kChunk; ++j)
 #pragma unroll
         for (int k = 0; k < PER; ++k) o[k] = wv[j] != 0.f ? fmaf(wv[j], pv[j][k], o[k]) : o[k];
     }
@@ -1241,8 +1243,12 @@ void launch_stream(DecodeParams p, hipStream_t s) {
   else
     hipLaunchKernelGGL((paged_decode_stream<Tag, D, G, false>), dim3(static_cast<unsigned>(wgs)),
                        dim3(64 * kStreamWaves), 0, s, p);
-  hipLaunchKernelGGL((paged_decode_merge_stream<Tag, D>),
-                     dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(64), 0, s, p);
+  if (p.shared_blocks != nullptr)
+    hipLaunchKernelGGL((paged_decode_merge_stream<Tag, D, 16>),
+                       dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(64), 0, s, p);
+  else
+    hipLaunchKernelGGL((paged_decode_merge_stream<Tag, D>),
+                       dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(64), 0, s, p);
 }
 
 template <class Tag, int D>
@@ -1357,18 +1363,20 @@ struct CascadeLayout {
   int64_t stream_rows, lse_off, cu_off, shared_off, total;
   int splits, split_keys;
 };
-constexpr int kPrefixSplitKeys = 512;  // keys per prefix split (a multiple of the prefill tile)
+constexpr int kPrefixSplitKeys = 1024;  // most keys per prefix split (a multiple of the prefill tile)
 CascadeLayout cascade_layout(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
                              int64_t page_block_size, int64_t shared_hint) {
   CascadeLayout c;
   int wgs = device_cu_count();
   wgs -= wgs % kXcds;
   c.stream_rows = 2 * static_cast<int64_t>(wgs) * (kStreamWaves / num_kv_heads) * num_heads;
-  // Splits of 512 keys, halved while the prefix pass would fill fewer than ~2 workgroups per CU.
+  // Splits of 1024 keys, halved (down to 256) while the prefix pass would fill fewer
+  // workgroups than CUs: each workgroup should walk enough 64-key tiles to hide its
+  // start (the shared-block scan, the queries, the first tiles' latency).
   const int64_t keys = std::max<int64_t>(shared_hint, 1) * page_block_size;
   const int64_t row_tiles = ceil_div(batch * (num_heads / num_kv_heads), 128);
   c.split_keys = kPrefixSplitKeys;
-  while (c.split_keys > 64 && ceil_div(keys, c.split_keys) * num_kv_heads * row_tiles < 2 * wgs) c.split_keys /= 2;
+  while (c.split_keys > 256 && ceil_div(keys, c.split_keys) * num_kv_heads * row_tiles < wgs) c.split_keys /= 2;
   c.splits = static_cast<int>(ceil_div(keys, c.split_keys));
   const int64_t rows = c.stream_rows + (c.splits + 1) * batch * num_heads;
   const WorkspaceLayout wl = workspace_layout(rows, head_dim);

@@ -112,6 +112,13 @@ def split_tokens(batch: int, num_kv_heads: int, max_seqlen_k: int, path: int | s
     return int(L.paged_decode_attention_path_split_tokens(path, batch, num_kv_heads, max_seqlen_k))
 
 
+def shared_prefix_workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                                 page_block_size: int, max_seqlen_k: int, shared_blocks_hint: int) -> int:
+    """Workspace bytes of a cascaded call (paged_decode_attention_shared_prefix)."""
+    return int(_lib.load().paged_decode_attention_shared_prefix_workspace_size(
+        batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k, shared_blocks_hint))
+
+
 # First-pass names of paged_decode_attention_path.
 DECODE_PATHS = {"auto": 0, "split": 1, "persistent": 2, "stream": 3, "rows": 4}
 
@@ -167,8 +174,7 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     if shared_prefix_blocks is not None:
         if path != 0 or noalloc:
             raise _lib.OxideError("shared_prefix_blocks takes no forced path and no noalloc")
-        need = int(L.paged_decode_attention_shared_prefix_workspace_size(B, Hq, Hkv, D, BS, max_seqlen_k,
-                                                                         int(shared_prefix_blocks)))
+        need = shared_prefix_workspace_size(B, Hq, Hkv, D, BS, max_seqlen_k, int(shared_prefix_blocks))
         if workspace is None or workspace.numel() * workspace.element_size() < need:
             workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
         kv = (None, None, None) if append is None else (_ptr(key), _ptr(value), _ptr(slot_mapping))

@@ -68,6 +68,23 @@ class DecodeStep:
         eff = np.minimum(L, c.window_left + 1) if c.window_left >= 0 else L
         return int(2 * eff.sum() * c.num_kv_heads * c.head_dim * elem)
 
+    def unique_kv_read_bytes(self, elem: int = 2) -> int:
+        """K+V bytes of the distinct cache rows the batch attends (window-limited): a
+        row that several sequences reach through a shared block counts once.  Equal
+        to kv_read_bytes() when no block is shared."""
+        c = self.cfg
+        L = self.context_lens.astype(np.int64)
+        lo = np.maximum(L - 1 - c.window_left, 0) if c.window_left >= 0 else np.zeros_like(L)
+        slots = [np.asarray(self.block_rows[b], np.int64)[np.arange(lo[b], L[b]) // c.block_size] * c.block_size
+                 + np.arange(lo[b], L[b]) % c.block_size for b in range(len(L))]
+        n = np.unique(np.concatenate(slots)).size if slots else 0
+        return int(2 * n * c.num_kv_heads * c.head_dim * elem)
+
+    def attn_unique_bytes(self, elem: int = 2) -> int:
+        """attn_bytes() with the K+V rows counted once per distinct cache row: the
+        least HBM traffic of a call that reads each shared row once."""
+        return self.attn_bytes(elem) - self.kv_read_bytes(elem) + self.unique_kv_read_bytes(elem)
+
     def attn_bytes(self, elem: int = 2) -> int:
         """Algorithmic bytes of one decode-attention call: K+V read, q read, out
         written, block-table entries and seqlens read."""
