@@ -694,8 +694,11 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
 // splits that intersect [lo, L) with log-sum-exp weights; each wave takes a
 // contiguous quarter of the splits and the quarters are combined in LDS.
 // Sequences with a single split were finished by pass 1 and are skipped;
-// empty sequences get zeros.
-template <class Tag, int D>
+// empty sequences get zeros.  A wave's log2-sum-exps and the partial rows of its
+// first kChunk splits are loaded in one round (clamped indices; weights select
+// the extra rows away), so the merge is two dependent rounds of loads after the
+// lengths, not three.
+template <class Tag, int D, int kChunk = 8>
 __global__ __launch_bounds__(kThreads) void paged_decode_merge(DecodeParams p) {
   constexpr int PER = D / 64;
   __shared__ float s_o[kWaves][D];
@@ -736,8 +739,18 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge(DecodeParams p) {
 
   const int64_t prow0 = (static_cast<int64_t>(b) * p.num_heads + h) * p.max_splits;
   const float* lse = p.part_lse + prow0;
-  float M = -INFINITY;
-  for (int sp = w_first + lane; sp <= w_last; sp += 64) M = fmaxf(M, lse[sp]);
+  const int wn = w_last - w_first + 1;  // this wave's splits (none when <= 0)
+  // One round: the lane's split lse and the wave's first kChunk partial rows.
+  const float lse_l = lane < wn ? lse[w_first + lane] : -INFINITY;
+  float pv0[kChunk][PER];
+#pragma unroll
+  for (int j = 0; j < kChunk; ++j) {
+    const float* po = p.part_o + (prow0 + min(w_first + j, last)) * D + lane;
+#pragma unroll
+    for (int k = 0; k < PER; ++k) pv0[j][k] = po[64 * k];
+  }
+  float M = lse_l;
+  for (int sp = w_first + 64 + lane; sp <= w_last; sp += 64) M = fmaxf(M, lse[sp]);  // more than 64 splits
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) M = fmaxf(M, __shfl_xor(M, m));
   const float msafe = M == -INFINITY ? 0.f : M;
@@ -746,21 +759,34 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge(DecodeParams p) {
   for (int i = 0; i < PER; ++i) o[i] = 0.f;
   float wsum = 0.f;
   // Groups of 64 splits: lane i owns the weight of split g + i, which every
-  // lane reads with a scalar readlane while several partial rows are in flight.
+  // lane reads with a scalar readlane; kChunk partial rows in flight at a time.
   for (int g = w_first; g <= w_last; g += 64) {
     const int cnt = min(64, w_last - g + 1);
-    const float wl = lane < cnt ? __builtin_amdgcn_exp2f(lse[g + lane] - msafe) : 0.f;
+    const float lg = g == w_first ? lse_l : (lane < cnt ? lse[g + lane] : -INFINITY);
+    const float wl = lg != -INFINITY ? __builtin_amdgcn_exp2f(lg - msafe) : 0.f;
     float ws = wl;
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ws += __shfl_xor(ws, m);
     wsum += ws;
-    const float* po = p.part_o + (prow0 + g) * D + lane;
-#pragma unroll 8
-    for (int i = 0; i < cnt; ++i) {
-      const float w =
-          __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i));
+    for (int i0 = 0; i0 < cnt; i0 += kChunk) {
+      float wv[kChunk], pv[kChunk][PER];
 #pragma unroll
-      for (int k = 0; k < PER; ++k) o[k] = fmaf(w, po[static_cast<int64_t>(i) * D + 64 * k], o[k]);
+      for (int j = 0; j < kChunk; ++j) {
+        const int i = i0 + j;
+        wv[j] = i < cnt ? __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wl), i)) : 0.f;
+        if (g == w_first && i0 == 0) {
+#pragma unroll
+          for (int k = 0; k < PER; ++k) pv[j][k] = pv0[j][k];
+        } else {
+          const float* po = p.part_o + (prow0 + g + min(i, cnt - 1)) * D + lane;
+#pragma unroll
+          for (int k = 0; k < PER; ++k) pv[j][k] = po[64 * k];
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j)
+#pragma unroll
+        for (int k = 0; k < PER; ++k) o[k] = wv[j] != 0.f ? fmaf(wv[j], pv[j][k], o[k]) : o[k];
     }
   }
 #pragma unroll
