@@ -180,7 +180,7 @@ int64_t paged_decode_attention_split_tokens(int64_t batch, int64_t num_kv_heads,
  * paged_decode_attention_append (all three given) with the first pass chosen
  * by the caller instead of by shape.  No counterpart in the reference; for
  * tuning and tests.  The choice is an argument of this call only: the library
- * keeps no state between calls.  path: 0 = by shape (as the plain entries),
+ * keeps no state between calls that changes what a call computes.  path: 0 = by shape (as the plain entries),
  * 1 = the split grid, 2 = the persistent pass, 3 = the stream pass where the
  * kv heads divide 8 (else the persistent pass), 4 = the row pass where the shape
  * allows it (head_dim 128, 8 kv heads, 32 query heads, power-of-two pages, at
@@ -220,6 +220,13 @@ int64_t paged_decode_attention_path_split_tokens(int path, int64_t batch, int64_
  * stream pass does not take (kv heads not dividing 8, more than 4096 sequences)
  * run the plain entries.  workspace: paged_decode_attention_shared_prefix_workspace_size
  * bytes.  Other arguments as for paged_decode_attention_append.
+ * When the per-sequence part is long enough to hide it, the shared-key pass runs
+ * beside the stream pass on a side stream the library keeps per device (created
+ * on the first such call, default priority), forked from `stream` and joined back
+ * into it with two events: all work is still ordered after what `stream` held
+ * before the call and before what it receives after, and under HIP graph capture
+ * the fork and join become graph edges.  Calls from several host threads are
+ * serialised only while they enqueue.
  */
 void paged_decode_attention_shared_prefix(void* out, const void* q, const void* key, const void* value,
                                           const int64_t* slot_mapping, void* k_cache, void* v_cache,

@@ -9,6 +9,9 @@ diverge early, a sequence shorter than the shared prefix, an empty sequence (no
 cascade), windows that start inside and past the prefix, page sizes 16 / 64 / 256,
 groups 1 / 2 / 4 / 8 / 16, D 64 / 128, f16 and bf16, the fused append (bit-identical
 cache, the new token attended), and the full-size cfg4 step through both entries.
+The last four cases (and cfg4) have private parts long enough that the library runs
+the prefix pass beside the stream pass on a side stream; the others run them one
+after the other.  Both passes find the shared count themselves.
 Tolerance: the target's (max-abs 2e-2, max-rel 1e-2) and the output-scaled bar.
 """
 import math
@@ -71,6 +74,12 @@ CASES = [
     (3, 4, 2, 64, 64, 5, [70, 1, 129], 200, 5, "f16", None),                      # G 2, D 64
     (3, 32, 2, 64, 32, 6, [5, 90, 33], -1, 6, "bf16", None),                      # G 16
     (130, 32, 8, 128, 256, 2, list(range(1, 131)), -1, 2, "bf16", None),          # 2 row tiles
+    # Long enough private parts that the prefix pass runs beside the stream pass on
+    # a side stream (the overlapped form):
+    (32, 32, 8, 128, 256, 4, [4096 - 97 * i for i in range(30)] + [-1024, -500], -1, 4, "bf16", None),
+    (32, 32, 8, 128, 256, 4, [4096 - 97 * i for i in range(30)] + [-1024, -500], 3000, 6, "f16", {5: 1}),
+    (16, 64, 8, 128, 256, 3, [8000 - 333 * i for i in range(16)], -1, 3, "bf16", None),             # G 8
+    (24, 32, 8, 128, 64, 12, [5000 + 5 * i for i in range(24)], 1500, 12, "bf16", {0: 11}),        # BS 64
 ]
 
 
@@ -188,3 +197,45 @@ def test_cascade_cfg4_full_size(device, fused):
                                             np.arange(len(ids), dtype=np.int32)[None], scale, c.window_left,
                                             threads=16)
         assert_attn_close(g_np[b:b + 1], ref)
+
+
+def test_cascade_overlapped_under_graph_capture(device):
+    """An overlapped cascaded call (prefix pass forked onto the library's side stream and
+    joined back) captured into a HIP graph on torch's capture stream: three replays with
+    eager cascaded calls and host synchronisations between them, each replay's output
+    bit-identical to the eager call on the same inputs."""
+    import torch
+    import oxide_paged_kv as ox
+
+    case = CASES[12]
+    B, Hq, Hkv, D, BS, shared, extra, window, hint, dtype, diverge = case
+    q, kc, vc, cu, table, mx, lens = _shared_case(21, B, Hq, Hkv, D, BS, shared, extra, dtype, diverge)
+    t = lambda a: to_torch(a, dtype, device)  # noqa: E731
+    cu_d = torch.from_numpy(cu.view(np.int32)).to(device)
+    bt_d = torch.from_numpy(table).to(device)
+    qd, kd, vd = t(q), t(kc), t(vc)
+    scale = 1 / math.sqrt(D)
+    ws = torch.zeros(ox.shared_prefix_workspace_size(B, Hq, Hkv, D, BS, mx, hint), dtype=torch.uint8, device=device)
+    want = ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, shared_prefix_blocks=hint)
+    out = torch.empty_like(qd)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):  # warm-up on the stream the capture will use
+        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, out=out, workspace=ws, shared_prefix_blocks=hint)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, out=out, workspace=ws, shared_prefix_blocks=hint)
+    for rep in range(3):
+        out.fill_(0)
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"cascade graph replay {rep}", flush=True)
+        assert torch.equal(out.view(torch.int16), want.view(torch.int16)), rep
+        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, shared_prefix_blocks=hint)
+        torch.cuda.synchronize()
+    got = to_f32(out)
+    ref = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype)
+    assert_attn_close(got, ref)

@@ -53,6 +53,13 @@ struct DecodeParams {
   int pre_splits;
   int split_keys;
   int64_t whole_row0;  // pre_row0 + pre_splits * batch * Hq; -1 without a cascade
+  // Cascaded call: the caller's upper bound on the shared entries (0 otherwise).
+  // The stream pass finds the shared count itself (find_shared_blocks, the same
+  // function and inputs as the prefix pass), so it need not wait for that pass.
+  int shared_hint;
+  // Stream pass workgroups (a multiple of 8); 0 = one per CU.  Fewer when the
+  // prefix pass of a cascaded call runs beside it on the remaining CUs.
+  int stream_wgs;
 };
 
 // Shared-prefix pass of a cascaded decode call (paged_prefill.hip): attention of
@@ -147,6 +154,39 @@ __device__ __forceinline__ int64_t new_token_slot(const DecodeParams& p, int b) 
 template <bool kScalar>
 __device__ __forceinline__ typename BtEntry<kScalar>::type* block_row(const DecodeParams& p, int b) {
   return (typename BtEntry<kScalar>::type*)(p.block_table + static_cast<int64_t>(b) * p.max_blocks);
+}
+
+// Cascaded calls: the number of leading block-table entries that are the same
+// block ids in every row of the batch, at most hint, and at most
+// (L_b - 1) / block_size for every sequence b (so each sequence keeps its newest
+// key outside the prefix; an empty sequence makes it 0).  Called by every thread
+// of a workgroup of kT threads; the lengths and the table entries are read in
+// one round of loads (entries up to hint, within every row since hint <=
+// max_blocks) and reduced through one LDS minimum, which every thread returns.
+// The prefix pass and the stream pass both call it on the same inputs, so they
+// agree on the count without waiting for each other.
+template <int kT>
+__device__ __forceinline__ int find_shared_blocks(const uint32_t* cu_seqlens_k, const int32_t* block_table,
+                                                  int64_t max_blocks, int batch, int block_size, int max_seqlen_k,
+                                                  int hint) {
+  __shared__ int s_min;
+  if (threadIdx.x == 0) s_min = hint;
+  __syncthreads();
+  int m = hint;
+  for (int b = threadIdx.x; b < batch; b += kT) {
+    const int64_t n = static_cast<int64_t>(cu_seqlens_k[b + 1]) - cu_seqlens_k[b];
+    const int L = static_cast<int>(n < 0 ? 0 : (n > max_seqlen_k ? max_seqlen_k : n));
+    m = min(m, L > 0 ? (L - 1) / block_size : 0);
+  }
+  const int64_t total = static_cast<int64_t>(batch - 1) * hint;
+  for (int64_t x = threadIdx.x; x < total; x += kT) {
+    const int64_t b = 1 + x / hint;
+    const int j = static_cast<int>(x % hint);
+    if (block_table[b * max_blocks + j] != block_table[j]) m = min(m, j);
+  }
+  atomicMin(&s_min, m);
+  __syncthreads();
+  return s_min;
 }
 
 // Largest b in [0, batch) with cu[b] <= key (cu non-decreasing).

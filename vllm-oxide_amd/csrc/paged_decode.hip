@@ -583,13 +583,18 @@ __global__ __launch_bounds__(64 * kStreamWaves, 1) void paged_decode_stream(Deco
   // sequence, laid end to end, cu holding their prefix sums and win_lo the lo_b
   // -- so keys before a window start weigh nothing in the balance.
   __shared__ int win_lo[kStreamCuLds];
-  // A cascaded call attends only the keys past the shared prefix here (its
-  // prefix pass wrote the number of shared blocks): ranges over attended keys.
-  const bool windowed = p.window_left >= 0 || p.shared_blocks != nullptr;
+  // A cascaded call attends only the keys past the shared prefix here (the
+  // shared count found as the prefix pass finds it): ranges over attended keys.
+  const bool windowed = p.window_left >= 0 || p.shared_hint > 0;
   if (!windowed) {
     for (int i = threadIdx.x; i <= p.batch; i += 64 * kStreamWaves) cu[i] = p.cu_seqlens_k[i];
   } else {
-    attended_prefix<64 * kStreamWaves>(p, cu, win_lo, p.shared_blocks ? *p.shared_blocks * p.block_size : 0);
+    const int floor_keys = p.shared_hint > 0 ? find_shared_blocks<64 * kStreamWaves>(
+                                                   p.cu_seqlens_k, p.block_table, p.max_blocks, p.batch,
+                                                   p.block_size, p.max_seqlen_k, p.shared_hint) *
+                                                   p.block_size
+                                             : 0;
+    attended_prefix<64 * kStreamWaves>(p, cu, win_lo, floor_keys);
   }
   __syncthreads();  // the last barrier: before any wave can leave
   // The merge's copy of the sums (after the barrier: every thread's runs are in).
@@ -1248,9 +1253,9 @@ bool dispatch_persistent(const DecodeParams& p, int group, hipStream_t s) {
 }
 
 template <class Tag, int D, int G>
-void launch_stream(DecodeParams p, hipStream_t s) {
+bool launch_stream(DecodeParams p, hipStream_t s, hipEvent_t join) {
   // One workgroup of 8 waves per CU; 8 / Hkv key ranges per workgroup and head.
-  int wgs = device_cu_count();
+  int wgs = p.stream_wgs > 0 ? p.stream_wgs : device_cu_count();
   wgs -= wgs % kXcds;  // a whole number of workgroups per XCD
   p.num_wgs = wgs * (kStreamWaves / p.num_kv_heads);
   // Two tiles in flight per wave (kDeep) for ranges shorter than 1536 keys by
@@ -1269,32 +1274,43 @@ void launch_stream(DecodeParams p, hipStream_t s) {
   else
     hipLaunchKernelGGL((paged_decode_stream<Tag, D, G, false>), dim3(static_cast<unsigned>(wgs)),
                        dim3(64 * kStreamWaves), 0, s, p);
+  if (join != nullptr) {
+    const hipError_t e = hipStreamWaitEvent(s, join, 0);
+    if (e != hipSuccess) {
+      oxide::set_error(OXIDE_ERR_HIP + static_cast<int>(e));
+      return true;  // the error is set; nothing more is launched
+    }
+  }
   if (p.shared_blocks != nullptr)
     hipLaunchKernelGGL((paged_decode_merge_stream<Tag, D, 16>),
                        dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(64), 0, s, p);
   else
     hipLaunchKernelGGL((paged_decode_merge_stream<Tag, D>),
                        dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(64), 0, s, p);
+  return true;
 }
 
 template <class Tag, int D>
-bool dispatch_stream(const DecodeParams& p, int group, hipStream_t s) {
+bool dispatch_stream(const DecodeParams& p, int group, hipStream_t s, hipEvent_t join) {
   switch (group) {
-    case 1: launch_stream<Tag, D, 1>(p, s); return true;
-    case 2: launch_stream<Tag, D, 2>(p, s); return true;
-    case 3: launch_stream<Tag, D, 3>(p, s); return true;
-    case 4: launch_stream<Tag, D, 4>(p, s); return true;
-    case 5: launch_stream<Tag, D, 5>(p, s); return true;
-    case 6: launch_stream<Tag, D, 6>(p, s); return true;
-    case 7: launch_stream<Tag, D, 7>(p, s); return true;
-    case 8: launch_stream<Tag, D, 8>(p, s); return true;
-    case 16: launch_stream<Tag, D, 16>(p, s); return true;
+    case 1: return launch_stream<Tag, D, 1>(p, s, join);
+    case 2: return launch_stream<Tag, D, 2>(p, s, join);
+    case 3: return launch_stream<Tag, D, 3>(p, s, join);
+    case 4: return launch_stream<Tag, D, 4>(p, s, join);
+    case 5: return launch_stream<Tag, D, 5>(p, s, join);
+    case 6: return launch_stream<Tag, D, 6>(p, s, join);
+    case 7: return launch_stream<Tag, D, 7>(p, s, join);
+    case 8: return launch_stream<Tag, D, 8>(p, s, join);
+    case 16: return launch_stream<Tag, D, 16>(p, s, join);
     default: return false;
   }
 }
 
+// join (cascaded calls whose prefix pass runs on a side stream): an event the
+// stream path's merge waits for; null otherwise.
 template <class Tag>
-bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hipStream_t s) {
+bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hipStream_t s,
+              hipEvent_t join = nullptr) {
   if (p.max_splits == 0) {
     // max_seqlen_k == 0: every sequence is empty, the output is zeros.
     const int64_t n = batch * p.num_heads * head_dim;
@@ -1315,8 +1331,8 @@ bool dispatch(const DecodeParams& p, int64_t batch, int head_dim, int group, hip
     return true;
   }
   if (p.split_tokens < 0) {
-    if (head_dim == 128) return dispatch_stream<Tag, 128>(p, group, s);
-    if (head_dim == 64) return dispatch_stream<Tag, 64>(p, group, s);
+    if (head_dim == 128) return dispatch_stream<Tag, 128>(p, group, s, join);
+    if (head_dim == 64) return dispatch_stream<Tag, 64>(p, group, s, join);
     return false;
   }
   const dim3 mgrid(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(batch));
@@ -1385,24 +1401,49 @@ namespace {
 // rows ((splits + 1) per query row: the prefix splits, then the whole-sequence
 // partials of the stream pass), their log2-sum-exps, the attended-key prefix
 // sums, and the number of shared blocks the prefix pass found.
+//
+// Overlap: when the stream pass is long enough to hide it, the prefix pass runs
+// beside it on a side stream (reserve CUs held back from the stream pass's grid)
+// in 2048-key splits, few enough workgroups to fit those CUs two per CU.
+// Otherwise the two run one after the other, the prefix pass over all CUs.
+// Rates measured on MI355X (Qwen3-8B heads, 128 sequences sharing 15 blocks of
+// 256 keys, window 4096): a prefix workgroup walks a 64-key tile in ~2.7 us two to
+// a CU and starts in ~10 us; the stream pass reads at ~4.5 TB/s beside it.  The
+// stream estimate takes every sequence at max_seqlen_k (the host knows no more),
+// so ragged batches lean towards overlapping.  That batch: 272 us plain, 122 us
+// one after the other, 107 us overlapped (48 CUs reserved, 64 prefix workgroups).
 struct CascadeLayout {
   int64_t stream_rows, lse_off, cu_off, shared_off, total;
   int splits, split_keys;
+  int reserve;  // CUs held back from the stream pass for the prefix pass; 0 = one after the other
 };
 constexpr int kPrefixSplitKeys = 1024;  // most keys per prefix split (a multiple of the prefill tile)
+constexpr int kOverlapSplitKeys = 2048;
 CascadeLayout cascade_layout(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-                             int64_t page_block_size, int64_t shared_hint) {
+                             int64_t page_block_size, int64_t max_seqlen_k, int64_t shared_hint) {
   CascadeLayout c;
   int wgs = device_cu_count();
   wgs -= wgs % kXcds;
   c.stream_rows = 2 * static_cast<int64_t>(wgs) * (kStreamWaves / num_kv_heads) * num_heads;
-  // Splits of 1024 keys, halved (down to 256) while the prefix pass would fill fewer
-  // workgroups than CUs: each workgroup should walk enough 64-key tiles to hide its
-  // start (the shared-block scan, the queries, the first tiles' latency).
   const int64_t keys = std::max<int64_t>(shared_hint, 1) * page_block_size;
   const int64_t row_tiles = ceil_div(batch * (num_heads / num_kv_heads), 128);
-  c.split_keys = kPrefixSplitKeys;
-  while (c.split_keys > 256 && ceil_div(keys, c.split_keys) * num_kv_heads * row_tiles < wgs) c.split_keys /= 2;
+  const int64_t ovl_wgs = ceil_div(keys, kOverlapSplitKeys) * num_kv_heads * row_tiles;
+  const int64_t reserve = ceil_div(ceil_div(ovl_wgs * 3, 4), kXcds) * kXcds;
+  const double stream_us = static_cast<double>(batch) * num_kv_heads *
+                           static_cast<double>(std::max<int64_t>(max_seqlen_k - keys, 0)) * 4.0 * head_dim / 4.5e6;
+  const double prefix_us = 10.0 + kOverlapSplitKeys / 64 * 2.7;
+  if (stream_us >= prefix_us && reserve <= wgs / 4) {
+    c.reserve = static_cast<int>(reserve);
+    c.split_keys = kOverlapSplitKeys;
+  } else {
+    // One after the other: splits of 1024 keys, halved (down to 256) while the prefix
+    // pass would fill fewer workgroups than CUs: each workgroup should walk enough
+    // 64-key tiles to hide its start (the shared-block scan, the queries, the first
+    // tiles' latency).
+    c.reserve = 0;
+    c.split_keys = kPrefixSplitKeys;
+    while (c.split_keys > 256 && ceil_div(keys, c.split_keys) * num_kv_heads * row_tiles < wgs) c.split_keys /= 2;
+  }
   c.splits = static_cast<int>(ceil_div(keys, c.split_keys));
   const int64_t rows = c.stream_rows + (c.splits + 1) * batch * num_heads;
   const WorkspaceLayout wl = workspace_layout(rows, head_dim);
@@ -1411,6 +1452,34 @@ CascadeLayout cascade_layout(int64_t batch, int64_t num_heads, int64_t num_kv_he
   c.shared_off = c.cu_off + ceil_div((batch + 1) * 4, 256) * 256;
   c.total = c.shared_off + 256;
   return c;
+}
+
+// The side stream of overlapped cascaded calls on each device, with the two
+// events that fork it from and join it back into the caller's stream (both are
+// capturable: under HIP graph capture the fork and the join become graph edges).
+// Created on a device's first overlapped call and kept for the process, at the
+// default priority.  Callers hold g_side_mutex from the fork to the join's
+// enqueue, so calls from several host threads each wait for their own work.
+struct SideStream {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool tried = false, ok = false;
+};
+constexpr int kMaxSideDevices = 64;
+std::mutex g_side_mutex;
+SideStream g_side[kMaxSideDevices];
+SideStream* side_stream_locked() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxSideDevices) return nullptr;
+  SideStream& t = g_side[dev];
+  if (!t.tried) {
+    t.tried = true;
+    oxide::RelaxedCaptureScope relaxed;
+    t.ok = hipStreamCreateWithFlags(&t.stream, hipStreamNonBlocking) == hipSuccess &&
+           hipEventCreateWithFlags(&t.fork, hipEventDisableTiming) == hipSuccess &&
+           hipEventCreateWithFlags(&t.join, hipEventDisableTiming) == hipSuccess;
+  }
+  return t.ok ? &t : nullptr;
 }
 }  // namespace
 
@@ -1422,7 +1491,7 @@ extern "C" size_t paged_decode_attention_shared_prefix_workspace_size(int64_t ba
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0 ||
       page_block_size <= 0 || shared_blocks_hint <= 0 || num_heads % num_kv_heads != 0)
     return plain;
-  const CascadeLayout c = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size,
+  const CascadeLayout c = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k,
                                          std::min(shared_blocks_hint, ceil_div(max_seqlen_k, page_block_size)));
   return std::max(plain, static_cast<size_t>(c.total));
 }
@@ -1496,7 +1565,8 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
     // the rest by the stream pass, both merged by the stream merge.
     // Never more shared blocks than the longest sequence has (the size query clamps alike).
     shared_hint = std::min(shared_hint, ceil_div(max_seqlen_k, page_block_size));
-    const CascadeLayout cl = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, shared_hint);
+    const CascadeLayout cl =
+        cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k, shared_hint);
     if (workspace_bytes < static_cast<size_t>(cl.total) || !workspace) {
       oxide::set_error(OXIDE_ERR_WORKSPACE_TOO_SMALL);
       return;
@@ -1516,6 +1586,7 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
     p.pre_splits = cl.splits;
     p.split_keys = cl.split_keys;
     p.whole_row0 = cl.stream_rows + static_cast<int64_t>(cl.splits) * batch * num_heads;
+    p.shared_hint = static_cast<int>(shared_hint);
     p.out = out;
     p.new_k = new_k;
     p.new_v = new_v;
@@ -1557,10 +1628,38 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
     a.shared_hint = static_cast<int>(shared_hint);
     a.shared_out = reinterpret_cast<int*>(ws + cl.shared_off);
     a.bf16 = dtype == OXIDE_DTYPE_BF16;
-    const bool ok = oxide::launch_decode_prefix(a, s) &&
-                    (dtype == OXIDE_DTYPE_BF16
-                         ? dispatch<Bf16Tag>(p, batch, static_cast<int>(head_dim), static_cast<int>(group), s)
-                         : dispatch<F16Tag>(p, batch, static_cast<int>(head_dim), static_cast<int>(group), s));
+    auto pass1_and_merge = [&](hipEvent_t join) {
+      return dtype == OXIDE_DTYPE_BF16
+                 ? dispatch<Bf16Tag>(p, batch, static_cast<int>(head_dim), static_cast<int>(group), s, join)
+                 : dispatch<F16Tag>(p, batch, static_cast<int>(head_dim), static_cast<int>(group), s, join);
+    };
+    bool ok = false, overlapped = false;
+    if (cl.reserve > 0) {
+      // The prefix pass on the side stream, the stream pass on the caller's stream
+      // over the other CUs; the merge waits for both.
+      std::lock_guard<std::mutex> lock(g_side_mutex);
+      SideStream* side = side_stream_locked();
+      if (side != nullptr) {
+        int wgs = device_cu_count();
+        wgs -= wgs % kXcds;
+        p.stream_wgs = wgs - cl.reserve;
+        const hipError_t e1 = hipEventRecord(side->fork, s);
+        const hipError_t e2 = e1 == hipSuccess ? hipStreamWaitEvent(side->stream, side->fork, 0) : e1;
+        if (e2 != hipSuccess) {
+          oxide::set_error(OXIDE_ERR_HIP + static_cast<int>(e2));
+          return;
+        }
+        ok = oxide::launch_decode_prefix(a, side->stream);
+        const hipError_t e3 = hipEventRecord(side->join, side->stream);
+        if (e3 != hipSuccess) {
+          oxide::set_error(OXIDE_ERR_HIP + static_cast<int>(e3));
+          return;
+        }
+        ok = ok && pass1_and_merge(side->join);
+        overlapped = true;
+      }
+    }
+    if (!overlapped) ok = oxide::launch_decode_prefix(a, s) && pass1_and_merge(nullptr);
     if (!ok) {
       oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
       return;

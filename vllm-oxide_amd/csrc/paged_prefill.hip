@@ -98,31 +98,6 @@ __device__ __forceinline__ int clamp_len(int64_t n, int cap) {
   return static_cast<int>(n < 0 ? 0 : (n > cap ? cap : n));
 }
 
-// Shared-prefix pass: the number of leading block-table entries identical in every
-// row of the decode batch, at most shared_hint, and at most (L_b - 1) / block_size
-// for every sequence b (so each sequence keeps at least its newest key outside the
-// prefix; an empty sequence makes it 0).  Every workgroup computes it the same way
-// (a scan of batch x shared_hint table entries, cooperative, through LDS minima).
-__device__ __forceinline__ int shared_prefix_blocks(const PrefillParams& p) {
-  __shared__ int s_blocks;
-  if (threadIdx.x == 0) s_blocks = p.shared_hint;
-  __syncthreads();
-  for (int b = threadIdx.x; b < p.dec_batch; b += kPfThreads) {
-    const int L = clamp_len(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - p.cu_seqlens_k[b], p.max_seqlen_k);
-    atomicMin(&s_blocks, L > 0 ? (L - 1) / p.block_size : 0);
-  }
-  __syncthreads();
-  const int n0 = s_blocks;
-  const int64_t total = static_cast<int64_t>(p.dec_batch - 1) * n0;
-  for (int64_t x = threadIdx.x; x < total; x += kPfThreads) {
-    const int64_t b = 1 + x / n0;
-    const int jj = static_cast<int>(x % n0);
-    if (p.block_table[b * p.max_blocks + jj] != p.block_table[jj]) atomicMin(&s_blocks, jj);
-  }
-  __syncthreads();
-  return s_blocks;
-}
-
 // LDS tile layouts (64 keys, row = one key's head slice of 2*D bytes):
 //   K: 16-byte chunk c of row r at chunk position c ^ kswz(r).  One MFMA
 //      operand read (16 lanes = 16 consecutive rows, one chunk each) then
@@ -204,7 +179,8 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
 
   int Lq, Lk;
   if constexpr (kPrefix) {
-    const int shared = shared_prefix_blocks(p);
+    const int shared = find_shared_blocks<kPfThreads>(p.cu_seqlens_k, p.block_table, p.max_blocks, p.dec_batch,
+                                                      p.block_size, p.max_seqlen_k, p.shared_hint);
     if (blockIdx.x == 0 && threadIdx.x == 0) *p.shared_out = shared;
     Lq = p.dec_batch;
     Lk = shared * p.block_size;  // the shared keys; no sequence attends past them here
