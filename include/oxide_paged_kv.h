@@ -5,7 +5,9 @@
  * hipStream_t passed as `void*`.  Nothing here allocates device memory: the
  * caller owns every buffer, including the split-KV workspace of the decode
  * attention.  All launches are asynchronous on the given stream (NULL = the
- * default stream).  Entry points return void, as the reference's do; argument
+ * default stream), which belongs to the calling thread's current HIP device
+ * (the device whose CU count sizes the grids).  Entry points return void, as
+ * the reference's do; argument
  * and launch errors are recorded per host thread and read back with
  * oxide_last_error() / oxide_error_string().
  *
