@@ -943,8 +943,8 @@ __global__ __launch_bounds__(kThreads) void paged_decode_merge_persistent(Decode
 // per piece reads its log2-sum-exp, the weights are reduced across the wave,
 // and each lane then accumulates D / 64 output dims over the pieces, so the
 // whole merge is three dependent rounds of loads (lengths, lse, partials).
-// kChunk: pieces whose partial rows are loaded per round (16 for cascaded calls,
-// whose (sequence, head) rows also gather the prefix splits).
+// kChunk: pieces whose partial rows are loaded per round (16 for cascaded calls
+// with more than four prefix splits, whose (sequence, head) rows gather them all).
 template <class Tag, int D, int kChunk = 8>
 __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) {
   constexpr int PER = D / 64;
@@ -961,7 +961,9 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   // instead of one each.
   uint32_t c0 = p.cu_seqlens_k[b], c1 = p.cu_seqlens_k[b + 1], cn = p.cu_seqlens_k[p.batch];
   uint32_t a0 = p.attn_cu[b], a1 = p.attn_cu[b + 1], an = p.attn_cu[p.batch];
-  asm volatile("" : "+s"(c0), "+s"(c1), "+s"(cn), "+s"(a0), "+s"(a1), "+s"(an));
+  // A cascaded call's shared count joins the same round (the item count depends on it).
+  int shared = p.shared_blocks != nullptr ? *p.shared_blocks : 0;
+  asm volatile("" : "+s"(c0), "+s"(c1), "+s"(cn), "+s"(a0), "+s"(a1), "+s"(an), "+s"(shared));
   const int64_t cb = c0;
   const int64_t Lraw = max(static_cast<int64_t>(c1) - cb, int64_t{0});
   const int64_t N = cn;
@@ -1017,8 +1019,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_stream(DecodeParams p) 
   // Items: pass 1's pieces (a whole sequence of a cascaded call: its one partial
   // row at prefix split pre_splits), then the prefix splits that hold shared keys.
   const int n_s = whole ? 1 : static_cast<int>(wb - wa + 1);
-  const int n_p = cascade ? min(p.pre_splits, (*p.shared_blocks * p.block_size + p.split_keys - 1) / p.split_keys)
-                          : 0;
+  const int n_p = cascade ? min(p.pre_splits, (shared * p.block_size + p.split_keys - 1) / p.split_keys) : 0;
   const int n = n_s + n_p;
   auto pre_row = [&](int sp) -> int64_t {
     return p.pre_row0 + (static_cast<int64_t>(sp) * p.batch + b) * p.num_heads + h;
@@ -1281,7 +1282,8 @@ bool launch_stream(DecodeParams p, hipStream_t s, hipEvent_t join) {
       return true;  // the error is set; nothing more is launched
     }
   }
-  if (p.shared_blocks != nullptr)
+  // Cascaded calls with more than a few prefix splits gather more items per row.
+  if (p.shared_blocks != nullptr && p.pre_splits > 4)
     hipLaunchKernelGGL((paged_decode_merge_stream<Tag, D, 16>),
                        dim3(static_cast<unsigned>(p.num_heads), static_cast<unsigned>(p.batch)), dim3(64), 0, s, p);
   else
