@@ -216,7 +216,8 @@ int64_t paged_decode_attention_path_split_tokens(int path, int64_t batch, int64_
  * paged_decode_attention(_append) within rounding; no reference counterpart (the
  * reference reads the shared blocks once per sequence).
  * shared_blocks_hint: an upper bound on the leading entries shared by every row
- * (0 = no cascade: the plain entries run).  The kernels find the actual count on
+ * (0 = no cascade: the plain entries run; so do batches where the cascade would
+ * not pay, see paged_decode_attention_shared_prefix_plan).  The kernels find the actual count on
  * the device (identical block ids in every row, and at most (L_b - 1) / block_size
  * for every sequence), so a wrong hint costs time, never correctness.  Shapes the
  * stream pass does not take (kv heads not dividing 8, more than 4096 sequences)
@@ -238,6 +239,35 @@ void paged_decode_attention_shared_prefix(void* out, const void* q, const void* 
                                           int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left,
                                           float softmax_scale, int64_t shared_blocks_hint, void* workspace,
                                           size_t workspace_bytes, int dtype, void* stream);
+
+/*
+ * paged_decode_attention_shared_prefix with its form chosen by the caller instead
+ * of by shape.  No counterpart in the reference; for tuning and tests.  mode:
+ * 0 = by shape (as paged_decode_attention_shared_prefix), 1 = the cascade with
+ * its two passes one after the other, 2 = the cascade with the shared-key pass
+ * beside the per-sequence pass on the side stream, 3 = the plain entries; other
+ * values are OXIDE_ERR_INVALID_ARGUMENT.  Shapes the cascade does not take run
+ * the plain entries whatever the mode.  Results agree within rounding; the
+ * workspace size is the same for every mode.
+ */
+void paged_decode_attention_shared_prefix_mode(int mode, void* out, const void* q, const void* key,
+                                               const void* value, const int64_t* slot_mapping, void* k_cache,
+                                               void* v_cache, const uint32_t* cu_seqlens_k,
+                                               const int32_t* block_table, int64_t max_blocks_per_seq,
+                                               int64_t num_blocks, int64_t batch, int64_t num_heads,
+                                               int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
+                                               int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
+                                               int64_t shared_blocks_hint, void* workspace, size_t workspace_bytes,
+                                               int dtype, void* stream);
+
+/* The form paged_decode_attention_shared_prefix (mode 0) takes on these
+ * arguments: 1, 2 or 3 as for paged_decode_attention_shared_prefix_mode.  The
+ * cascade runs only where the K/V bytes it saves (the shared keys read once
+ * instead of once per sequence) outweigh its extra pass; no reference
+ * counterpart. */
+int paged_decode_attention_shared_prefix_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                              int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k,
+                                              int64_t shared_blocks_hint);
 
 /* Bytes of workspace paged_decode_attention_shared_prefix needs (at least
  * paged_decode_attention_workspace_size, so the fallback fits too). */

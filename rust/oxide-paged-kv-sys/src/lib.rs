@@ -212,6 +212,47 @@ extern "C" {
         stream: HipStream,
     );
 
+    /// paged_decode_attention_shared_prefix with its form given: 0 by shape, 1 cascade one pass
+    /// after the other, 2 cascade overlapped, 3 plain entries.
+    pub fn paged_decode_attention_shared_prefix_mode(
+        mode: c_int,
+        out: *mut c_void,
+        q: *const c_void,
+        key: *const c_void,
+        value: *const c_void,
+        slot_mapping: *const i64,
+        k_cache: *mut c_void,
+        v_cache: *mut c_void,
+        cu_seqlens_k: *const u32,
+        block_table: *const i32,
+        max_blocks_per_seq: i64,
+        num_blocks: i64,
+        batch: i64,
+        num_heads: i64,
+        num_kv_heads: i64,
+        head_dim: i64,
+        page_block_size: i64,
+        max_seqlen_k: i64,
+        window_left: i32,
+        softmax_scale: f32,
+        shared_blocks_hint: i64,
+        workspace: *mut c_void,
+        workspace_bytes: usize,
+        dtype: c_int,
+        stream: HipStream,
+    );
+
+    /// The form paged_decode_attention_shared_prefix takes: 1, 2 or 3 as above.
+    pub fn paged_decode_attention_shared_prefix_plan(
+        batch: i64,
+        num_heads: i64,
+        num_kv_heads: i64,
+        head_dim: i64,
+        page_block_size: i64,
+        max_seqlen_k: i64,
+        shared_blocks_hint: i64,
+    ) -> c_int;
+
     pub fn paged_decode_attention_shared_prefix_workspace_size(
         batch: i64,
         num_heads: i64,

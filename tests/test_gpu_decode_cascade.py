@@ -9,9 +9,11 @@ diverge early, a sequence shorter than the shared prefix, an empty sequence (no
 cascade), windows that start inside and past the prefix, page sizes 16 / 64 / 256,
 groups 1 / 2 / 4 / 8 / 16, D 64 / 128, f16 and bf16, the fused append (bit-identical
 cache, the new token attended), and the full-size cfg4 step through both entries.
-The last four cases (and cfg4) have private parts long enough that the library runs
-the prefix pass beside the stream pass on a side stream; the others run them one
-after the other.  Both passes find the shared count themselves.
+Every case runs through both forms of the cascade, forced (the two passes one after the
+other, and the prefix pass beside the stream pass on the library's side stream): by
+shape these batches save too few bytes and would run the plain entries; the cfg4 test
+runs the form chosen by shape (overlapped).  Both passes find the shared count
+themselves.
 Tolerance: the target's (max-abs 2e-2, max-rel 1e-2) and the output-scaled bar.
 """
 import math
@@ -74,8 +76,8 @@ CASES = [
     (3, 4, 2, 64, 64, 5, [70, 1, 129], 200, 5, "f16", None),                      # G 2, D 64
     (3, 32, 2, 64, 32, 6, [5, 90, 33], -1, 6, "bf16", None),                      # G 16
     (130, 32, 8, 128, 256, 2, list(range(1, 131)), -1, 2, "bf16", None),          # 2 row tiles
-    # Long enough private parts that the prefix pass runs beside the stream pass on
-    # a side stream (the overlapped form):
+    # Longer private parts (by shape the overlap would be chosen if the batch saved
+    # enough bytes to take the cascade at all):
     (32, 32, 8, 128, 256, 4, [4096 - 97 * i for i in range(30)] + [-1024, -500], -1, 4, "bf16", None),
     (32, 32, 8, 128, 256, 4, [4096 - 97 * i for i in range(30)] + [-1024, -500], 3000, 6, "f16", {5: 1}),
     (16, 64, 8, 128, 256, 3, [8000 - 333 * i for i in range(16)], -1, 3, "bf16", None),             # G 8
@@ -83,7 +85,7 @@ CASES = [
 ]
 
 
-def _run(device, case, append):
+def _run(device, case, append, mode="auto"):
     import torch
     import oxide_paged_kv as ox
 
@@ -118,20 +120,51 @@ def _run(device, case, append):
         app = (t(kn), t(vn), torch.from_numpy(slots).to(device))
     want = oracle.paged_decode_attention(q, kc2, vc2, cu, table, scale, window, dtype)
     kd, vd = t(kc), t(vc)
-    got = ox.decode_attn(t(q), kd, vd, cu_d, bt_d, mx, scale, w, BS, append=app, shared_prefix_blocks=hint)
+    got = ox.decode_attn(t(q), kd, vd, cu_d, bt_d, mx, scale, w, BS, append=app, shared_prefix_blocks=hint,
+                         shared_prefix_mode=mode)
     torch.cuda.synchronize()
     return to_f32(got), want, (to_bits(kd), to_bits(vd)), (kc2, vc2)
 
 
 @pytest.mark.parametrize("case", CASES, ids=[f"s{i}" for i in range(len(CASES))])
 @pytest.mark.parametrize("append", [False, True], ids=["plain", "append"])
-def test_cascade_vs_oracle(device, case, append):
-    print(f"cascade case {case[:7]} window={case[7]} hint={case[8]} {case[9]} append={append}", flush=True)
-    got, want, caches, want_caches = _run(device, case, append)
+@pytest.mark.parametrize("mode", ["serial", "overlap"])
+def test_cascade_vs_oracle(device, case, append, mode):
+    """Every case through both forms of the cascade, forced (by shape most of these small
+    batches would run the plain entries: the cascade saves them too few bytes)."""
+    print(f"cascade case {case[:7]} window={case[7]} hint={case[8]} {case[9]} append={append} {mode}", flush=True)
+    got, want, caches, want_caches = _run(device, case, append, mode)
     assert_attn_close(got, want)
     assert_attn_scaled(got, want, label=f"cascade {case[:5]}")
     if append:
         assert np.array_equal(caches[0], want_caches[0]) and np.array_equal(caches[1], want_caches[1])
+
+
+def test_cascade_plan_by_shape(device):
+    """The by-shape form: the plain entries where the cascade saves under 200 MB of K/V
+    reads (small batches), the cascade beyond, overlapped when the per-sequence part is long
+    (cfg4); shapes the stream pass does not take always run the plain entries.  A batch the
+    plan sends to the plain entries gives the plain entry's bits."""
+    import torch
+    import oxide_paged_kv as ox
+
+    assert ox.shared_prefix_plan(4, 32, 8, 128, 256, 8192 + 256, 32) == "plain"
+    assert ox.shared_prefix_plan(16, 32, 8, 128, 256, 2048 + 1024, 8) == "plain"
+    assert ox.shared_prefix_plan(32, 32, 8, 128, 256, 4096 + 2000, 16) != "plain"
+    assert ox.shared_prefix_plan(128, 32, 8, 128, 256, 5120, 16) == "overlap"
+    assert ox.shared_prefix_plan(128, 32, 6, 128, 256, 5120, 16) == "plain"  # kv heads not dividing 8
+    assert ox.shared_prefix_plan(128, 32, 8, 128, 256, 5120, 0) == "plain"
+    case = CASES[0]
+    B, Hq, Hkv, D, BS, shared, extra, window, hint, dtype, diverge = case
+    assert ox.shared_prefix_plan(B, Hq, Hkv, D, BS, shared * BS + max(extra), hint) == "plain"
+    q, kc, vc, cu, table, mx, lens = _shared_case(3, B, Hq, Hkv, D, BS, shared, extra, dtype, diverge)
+    t = lambda a: to_torch(a, dtype, device)  # noqa: E731
+    args = (t(q), t(kc), t(vc), torch.from_numpy(cu.view(np.int32)).to(device), torch.from_numpy(table).to(device),
+            mx, 1 / math.sqrt(D), None, BS)
+    a = to_bits(ox.decode_attn(*args, shared_prefix_blocks=hint))
+    b = to_bits(ox.decode_attn(*args))
+    torch.cuda.synchronize()
+    assert np.array_equal(a, b)
 
 
 def test_cascade_hint_zero_is_the_plain_entry(device):
@@ -216,25 +249,26 @@ def test_cascade_overlapped_under_graph_capture(device):
     qd, kd, vd = t(q), t(kc), t(vc)
     scale = 1 / math.sqrt(D)
     ws = torch.zeros(ox.shared_prefix_workspace_size(B, Hq, Hkv, D, BS, mx, hint), dtype=torch.uint8, device=device)
-    want = ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, shared_prefix_blocks=hint)
+    kw = dict(shared_prefix_blocks=hint, shared_prefix_mode="overlap")
+    want = ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, **kw)
     out = torch.empty_like(qd)
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):  # warm-up on the stream the capture will use
-        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, out=out, workspace=ws, shared_prefix_blocks=hint)
+        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, out=out, workspace=ws, **kw)
     torch.cuda.current_stream().wait_stream(s)
     torch.cuda.synchronize()
     assert torch.equal(out.view(torch.int16), want.view(torch.int16))
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
-        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, out=out, workspace=ws, shared_prefix_blocks=hint)
+        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, out=out, workspace=ws, **kw)
     for rep in range(3):
         out.fill_(0)
         g.replay()
         torch.cuda.synchronize()
         print(f"cascade graph replay {rep}", flush=True)
         assert torch.equal(out.view(torch.int16), want.view(torch.int16)), rep
-        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, shared_prefix_blocks=hint)
+        ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, scale, None, BS, **kw)
         torch.cuda.synchronize()
     got = to_f32(out)
     ref = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype)

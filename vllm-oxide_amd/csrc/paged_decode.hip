@@ -1421,8 +1421,23 @@ struct CascadeLayout {
 };
 constexpr int kPrefixSplitKeys = 1024;  // most keys per prefix split (a multiple of the prefill tile)
 constexpr int kOverlapSplitKeys = 2048;
+// Cascade modes (paged_decode_attention_shared_prefix_mode).
+enum CascadeMode { kCascadeAuto = 0, kCascadeSerial = 1, kCascadeOverlap = 2, kCascadePlain = 3 };
+// By shape (kCascadeAuto), the cascade runs only when the K/V bytes it saves -- the
+// shared keys read once instead of once per sequence -- are worth the prefix pass's
+// start-up.  Measured on MI355X (Qwen3-8B heads, page 256), plain vs cascaded:
+// B=4 sharing 8192 keys 32.1 vs 53.8 us, B=8 / 4096 34.9 vs 49.4, B=16 / 2048 34.5 vs
+// 45.8 (100-126 MB saved: plain wins); B=64 / 1024 129.4 vs 109.5 (264 MB), B=32 /
+// 4096 103.4 vs 64.8, B=256 / 1024 197.5 vs 104.0, B=16 / 16384 176.0 vs 56.9 (cascade
+// wins).  The threshold sits between: 200 MB.
+bool cascade_pays(int64_t batch, int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
+                  int64_t shared_hint) {
+  const double saved = static_cast<double>(batch - 1) * shared_hint * page_block_size * num_kv_heads * 4.0 * head_dim;
+  return saved >= 200e6;
+}
 CascadeLayout cascade_layout(int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-                             int64_t page_block_size, int64_t max_seqlen_k, int64_t shared_hint) {
+                             int64_t page_block_size, int64_t max_seqlen_k, int64_t shared_hint,
+                             int mode = kCascadeAuto) {
   CascadeLayout c;
   int wgs = device_cu_count();
   wgs -= wgs % kXcds;
@@ -1434,8 +1449,9 @@ CascadeLayout cascade_layout(int64_t batch, int64_t num_heads, int64_t num_kv_he
   const double stream_us = static_cast<double>(batch) * num_kv_heads *
                            static_cast<double>(std::max<int64_t>(max_seqlen_k - keys, 0)) * 4.0 * head_dim / 4.5e6;
   const double prefix_us = 10.0 + kOverlapSplitKeys / 64 * 2.7;
-  if (stream_us >= prefix_us && reserve <= wgs / 4) {
-    c.reserve = static_cast<int>(reserve);
+  const bool overlap = mode == kCascadeOverlap || (mode == kCascadeAuto && stream_us >= prefix_us && reserve <= wgs / 4);
+  if (overlap) {
+    c.reserve = static_cast<int>(std::min<int64_t>(reserve, wgs / 2));
     c.split_keys = kOverlapSplitKeys;
   } else {
     // One after the other: splits of 1024 keys, halved (down to 256) while the prefix
@@ -1497,9 +1513,29 @@ extern "C" size_t paged_decode_attention_shared_prefix_workspace_size(int64_t ba
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0 ||
       page_block_size <= 0 || shared_blocks_hint <= 0 || num_heads % num_kv_heads != 0)
     return plain;
-  const CascadeLayout c = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k,
-                                         std::min(shared_blocks_hint, ceil_div(max_seqlen_k, page_block_size)));
-  return std::max(plain, static_cast<size_t>(c.total));
+  const int64_t hint = std::min(shared_blocks_hint, ceil_div(max_seqlen_k, page_block_size));
+  const CascadeLayout c1 = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k,
+                                          hint, kCascadeSerial);
+  const CascadeLayout c2 = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k,
+                                          hint, kCascadeOverlap);
+  return std::max({plain, static_cast<size_t>(c1.total), static_cast<size_t>(c2.total)});
+}
+
+// The form paged_decode_attention_shared_prefix runs on these arguments: 1 = the
+// cascade with its two passes one after the other, 2 = the cascade with the prefix
+// pass beside the stream pass, 3 = the plain entries (no cascade).
+extern "C" int paged_decode_attention_shared_prefix_plan(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                                         int64_t head_dim, int64_t page_block_size,
+                                                         int64_t max_seqlen_k, int64_t shared_blocks_hint) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || max_seqlen_k <= 0 ||
+      page_block_size <= 0 || shared_blocks_hint <= 0 || num_heads % num_kv_heads != 0)
+    return kCascadePlain;
+  const int64_t group = num_heads / num_kv_heads;
+  if (!stream_ok(batch, num_kv_heads) || !(group <= 8 || group == 16)) return kCascadePlain;
+  const int64_t hint = std::min(shared_blocks_hint, ceil_div(max_seqlen_k, page_block_size));
+  if (!cascade_pays(batch, num_kv_heads, head_dim, page_block_size, hint)) return kCascadePlain;
+  const CascadeLayout c = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k, hint);
+  return c.reserve > 0 ? kCascadeOverlap : kCascadeSerial;
 }
 
 extern "C" int64_t paged_decode_attention_pass1(int path, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
@@ -1542,7 +1578,7 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
                            int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
                            int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left,
                            float softmax_scale, void* workspace, size_t workspace_bytes, int dtype,
-                           void* stream, int64_t shared_hint = 0) {
+                           void* stream, int64_t shared_hint = 0, int cascade_mode = kCascadeAuto) {
   if (dtype != OXIDE_DTYPE_BF16 && dtype != OXIDE_DTYPE_F16) {
     oxide::set_error(OXIDE_ERR_UNSUPPORTED_DTYPE);
     return;
@@ -1566,13 +1602,15 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
     oxide::set_error(OXIDE_ERR_UNSUPPORTED_SHAPE);
     return;
   }
-  if (shared_hint > 0 && max_seqlen_k > 0 && stream_ok(batch, num_kv_heads) && (group <= 8 || group == 16)) {
+  // Never more shared blocks than the longest sequence has (the size query clamps alike).
+  if (shared_hint > 0 && max_seqlen_k > 0) shared_hint = std::min(shared_hint, ceil_div(max_seqlen_k, page_block_size));
+  if (shared_hint > 0 && max_seqlen_k > 0 && cascade_mode != kCascadePlain && stream_ok(batch, num_kv_heads) &&
+      (group <= 8 || group == 16) &&
+      (cascade_mode != kCascadeAuto || cascade_pays(batch, num_kv_heads, head_dim, page_block_size, shared_hint))) {
     // Cascaded call: the shared prefix on the matrix cores once for the whole batch,
     // the rest by the stream pass, both merged by the stream merge.
-    // Never more shared blocks than the longest sequence has (the size query clamps alike).
-    shared_hint = std::min(shared_hint, ceil_div(max_seqlen_k, page_block_size));
-    const CascadeLayout cl =
-        cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k, shared_hint);
+    const CascadeLayout cl = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k,
+                                            shared_hint, cascade_mode);
     if (workspace_bytes < static_cast<size_t>(cl.total) || !workspace) {
       oxide::set_error(OXIDE_ERR_WORKSPACE_TOO_SMALL);
       return;
@@ -1757,7 +1795,8 @@ void decode_append_impl(bool compact_ws, int forced_path, void* out, const void*
                         const int32_t* block_table, int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch,
                         int64_t num_heads, int64_t num_kv_heads, int64_t head_dim, int64_t page_block_size,
                         int64_t max_seqlen_k, int32_t window_left, float softmax_scale, void* workspace,
-                        size_t workspace_bytes, int dtype, void* stream, int64_t shared_hint = 0) {
+                        size_t workspace_bytes, int dtype, void* stream, int64_t shared_hint = 0,
+                        int cascade_mode = kCascadeAuto) {
   if (batch > 0 && (!key || !value || !slot_mapping || !oxide::aligned16(key) ||
                     !oxide::aligned16(value))) {
     oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
@@ -1776,7 +1815,7 @@ void decode_append_impl(bool compact_ws, int forced_path, void* out, const void*
   decode_attention_impl(compact_ws, forced_path, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k,
                         block_table, max_blocks_per_seq, num_blocks, batch, num_heads,
                         num_kv_heads, head_dim, page_block_size, max_seqlen_k, window_left,
-                        softmax_scale, workspace, workspace_bytes, dtype, stream, shared_hint);
+                        softmax_scale, workspace, workspace_bytes, dtype, stream, shared_hint, cascade_mode);
 }
 }  // namespace
 
@@ -1792,13 +1831,13 @@ extern "C" void paged_decode_attention_append(
                      max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream);
 }
 
-extern "C" void paged_decode_attention_shared_prefix(
-    void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping, void* k_cache,
-    void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table, int64_t max_blocks_per_seq,
-    int64_t num_blocks, int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
-    int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
+extern "C" void paged_decode_attention_shared_prefix_mode(
+    int mode, void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping,
+    void* k_cache, void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table,
+    int64_t max_blocks_per_seq, int64_t num_blocks, int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+    int64_t head_dim, int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
     int64_t shared_blocks_hint, void* workspace, size_t workspace_bytes, int dtype, void* stream) {
-  if (shared_blocks_hint < 0) {
+  if (shared_blocks_hint < 0 || mode < kCascadeAuto || mode > kCascadePlain) {
     oxide::set_error(OXIDE_ERR_INVALID_ARGUMENT);
     return;
   }
@@ -1806,13 +1845,26 @@ extern "C" void paged_decode_attention_shared_prefix(
     decode_attention_impl(false, 0, out, q, nullptr, nullptr, nullptr, k_cache, v_cache, cu_seqlens_k, block_table,
                           max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
                           max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream,
-                          shared_blocks_hint);
+                          shared_blocks_hint, mode);
     return;
   }
   decode_append_impl(false, 0, out, q, key, value, slot_mapping, k_cache, v_cache, cu_seqlens_k, block_table,
                      max_blocks_per_seq, num_blocks, batch, num_heads, num_kv_heads, head_dim, page_block_size,
                      max_seqlen_k, window_left, softmax_scale, workspace, workspace_bytes, dtype, stream,
-                     shared_blocks_hint);
+                     shared_blocks_hint, mode);
+}
+
+extern "C" void paged_decode_attention_shared_prefix(
+    void* out, const void* q, const void* key, const void* value, const int64_t* slot_mapping, void* k_cache,
+    void* v_cache, const uint32_t* cu_seqlens_k, const int32_t* block_table, int64_t max_blocks_per_seq,
+    int64_t num_blocks, int64_t batch, int64_t num_heads, int64_t num_kv_heads, int64_t head_dim,
+    int64_t page_block_size, int64_t max_seqlen_k, int32_t window_left, float softmax_scale,
+    int64_t shared_blocks_hint, void* workspace, size_t workspace_bytes, int dtype, void* stream) {
+  paged_decode_attention_shared_prefix_mode(kCascadeAuto, out, q, key, value, slot_mapping, k_cache, v_cache,
+                                            cu_seqlens_k, block_table, max_blocks_per_seq, num_blocks, batch,
+                                            num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k,
+                                            window_left, softmax_scale, shared_blocks_hint, workspace,
+                                            workspace_bytes, dtype, stream);
 }
 
 extern "C" void paged_decode_attention_path(

@@ -35,6 +35,10 @@ SIGNATURES = {
     "paged_decode_attention_shared_prefix": (None, [
         _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
         ctypes.c_int32, ctypes.c_float, _i64, _p, ctypes.c_size_t, ctypes.c_int, _p]),
+    "paged_decode_attention_shared_prefix_mode": (None, [
+        ctypes.c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _i64,
+        ctypes.c_int32, ctypes.c_float, _i64, _p, ctypes.c_size_t, ctypes.c_int, _p]),
+    "paged_decode_attention_shared_prefix_plan": (ctypes.c_int, [_i64, _i64, _i64, _i64, _i64, _i64, _i64]),
     "paged_decode_attention_shared_prefix_workspace_size": (ctypes.c_size_t, [_i64, _i64, _i64, _i64, _i64, _i64,
                                                                               _i64]),
     "paged_decode_attention_split_tokens": (_i64, [_i64, _i64, _i64]),

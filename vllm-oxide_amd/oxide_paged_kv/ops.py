@@ -112,6 +112,18 @@ def split_tokens(batch: int, num_kv_heads: int, max_seqlen_k: int, path: int | s
     return int(L.paged_decode_attention_path_split_tokens(path, batch, num_kv_heads, max_seqlen_k))
 
 
+# Forms of a cascaded call (paged_decode_attention_shared_prefix_mode).
+CASCADE_MODES = {"auto": 0, "serial": 1, "overlap": 2, "plain": 3}
+
+
+def shared_prefix_plan(batch: int, num_heads: int, num_kv_heads: int, head_dim: int, page_block_size: int,
+                       max_seqlen_k: int, shared_blocks_hint: int) -> str:
+    """The form the by-shape cascaded call takes: "serial", "overlap" or "plain"."""
+    code = int(_lib.load().paged_decode_attention_shared_prefix_plan(
+        batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k, shared_blocks_hint))
+    return {v: k for k, v in CASCADE_MODES.items()}[code]
+
+
 def shared_prefix_workspace_size(batch: int, num_heads: int, num_kv_heads: int, head_dim: int,
                                  page_block_size: int, max_seqlen_k: int, shared_blocks_hint: int) -> int:
     """Workspace bytes of a cascaded call (paged_decode_attention_shared_prefix)."""
@@ -128,7 +140,8 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                 softmax_scale: float, window_left: int | None = None,
                 page_block_size: int = 256, out: torch.Tensor | None = None,
                 workspace: torch.Tensor | None = None, append=None, path: int | str = 0,
-                noalloc: bool = False, shared_prefix_blocks: int | None = None) -> torch.Tensor:
+                noalloc: bool = False, shared_prefix_blocks: int | None = None,
+                shared_prefix_mode: int | str = "auto") -> torch.Tensor:
     """Paged decode attention.
 
     q [B, Hq, D]; k_cache/v_cache [NB, page_block_size, Hkv, D]; cu_seqlens_k uint32-valued
@@ -143,6 +156,8 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
     shared_prefix_blocks: an upper bound on the leading block-table entries every row
     shares -> paged_decode_attention_shared_prefix (the shared keys attended once for the
     whole batch; the library finds the actual count); path must be "auto".
+    shared_prefix_mode: the cascade's form by name or code of CASCADE_MODES; anything but
+    "auto" goes through paged_decode_attention_shared_prefix_mode.
     """
     L = _lib.load()
     B, Hq, D = q.shape
@@ -178,10 +193,14 @@ def decode_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
         if workspace is None or workspace.numel() * workspace.element_size() < need:
             workspace = torch.empty(max(need, 1), dtype=torch.uint8, device=q.device)
         kv = (None, None, None) if append is None else (_ptr(key), _ptr(value), _ptr(slot_mapping))
-        L.paged_decode_attention_shared_prefix(
-            _ptr(out), _ptr(q), *kv, _ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k), _ptr(block_table), max_blocks,
-            NB, B, Hq, Hkv, D, BS, max_seqlen_k, w, float(softmax_scale), int(shared_prefix_blocks), _ptr(workspace),
-            workspace.numel() * workspace.element_size(), dtype_code(q.dtype), _stream(q))
+        mode = CASCADE_MODES[shared_prefix_mode] if isinstance(shared_prefix_mode, str) else int(shared_prefix_mode)
+        args = (_ptr(out), _ptr(q), *kv, _ptr(k_cache), _ptr(v_cache), _ptr(cu_seqlens_k), _ptr(block_table),
+                max_blocks, NB, B, Hq, Hkv, D, BS, max_seqlen_k, w, float(softmax_scale), int(shared_prefix_blocks),
+                _ptr(workspace), workspace.numel() * workspace.element_size(), dtype_code(q.dtype), _stream(q))
+        if mode == 0:
+            L.paged_decode_attention_shared_prefix(*args)
+        else:
+            L.paged_decode_attention_shared_prefix_mode(mode, *args)
         _lib.check()
         return out
     need = workspace_size(B, Hq, Hkv, D, max_seqlen_k)
