@@ -224,12 +224,13 @@ int64_t paged_decode_attention_path_split_tokens(int path, int64_t batch, int64_
  * run the plain entries.  workspace: paged_decode_attention_shared_prefix_workspace_size
  * bytes.  Other arguments as for paged_decode_attention_append.
  * When the per-sequence part is long enough to hide it, the shared-key pass runs
- * beside the stream pass on a side stream the library keeps per device (created
- * on the first such call, default priority), forked from `stream` and joined back
- * into it with two events: all work is still ordered after what `stream` held
- * before the call and before what it receives after, and under HIP graph capture
- * the fork and join become graph edges.  Calls from several host threads are
- * serialised only while they enqueue.
+ * beside the stream pass on a side stream the library keeps per host thread and
+ * device (created on the thread's first such call, default priority), forked from
+ * `stream` and joined back into it with two events: all work is still ordered
+ * after what `stream` held before the call and before what it receives after, and
+ * under HIP graph capture the fork and join become graph edges (one thread
+ * capturing two graphs at once, each with an overlapped call, would tie both to
+ * the same side stream: end one capture before the next call of the other).
  */
 void paged_decode_attention_shared_prefix(void* out, const void* q, const void* key, const void* value,
                                           const int64_t* slot_mapping, void* k_cache, void* v_cache,

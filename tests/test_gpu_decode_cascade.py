@@ -273,3 +273,50 @@ def test_cascade_overlapped_under_graph_capture(device):
     got = to_f32(out)
     ref = oracle.paged_decode_attention(q, kc, vc, cu, table, scale, window, dtype)
     assert_attn_close(got, ref)
+
+
+def test_cascade_overlapped_from_two_threads(device):
+    """Overlapped cascaded calls from two host threads at once, each on its own stream
+    (each thread forks onto its own side stream): every call's output bit-identical to
+    the same call made alone."""
+    import threading
+
+    import torch
+    import oxide_paged_kv as ox
+
+    case = CASES[12]
+    B, Hq, Hkv, D, BS, shared, extra, window, hint, dtype, diverge = case
+    q, kc, vc, cu, table, mx, lens = _shared_case(31, B, Hq, Hkv, D, BS, shared, extra, dtype, diverge)
+    t = lambda a: to_torch(a, dtype, device)  # noqa: E731
+    cu_d = torch.from_numpy(cu.view(np.int32)).to(device)
+    bt_d = torch.from_numpy(table).to(device)
+    kd, vd = t(kc), t(vc)
+    qs = [t(q), t(q[::-1].copy())]
+    kw = dict(shared_prefix_blocks=hint, shared_prefix_mode="overlap")
+    scale = 1 / math.sqrt(D)
+    want = [ox.decode_attn(qq, kd, vd, cu_d, bt_d, mx, scale, None, BS, **kw) for qq in qs]
+    torch.cuda.synchronize()
+    outs = [[None] * 5 for _ in range(2)]
+    errors = []
+
+    def work(i):
+        try:
+            s = torch.cuda.Stream()
+            ws = torch.zeros(ox.shared_prefix_workspace_size(B, Hq, Hkv, D, BS, mx, hint), dtype=torch.uint8,
+                             device=device)
+            with torch.cuda.stream(s):
+                for r in range(5):
+                    outs[i][r] = ox.decode_attn(qs[i], kd, vd, cu_d, bt_d, mx, scale, None, BS, workspace=ws, **kw)
+            s.synchronize()
+        except Exception as e:  # noqa: BLE001 -- reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(2)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join()
+    assert not errors, errors
+    for i in range(2):
+        for r in range(5):
+            assert torch.equal(outs[i][r].view(torch.int16), want[i].view(torch.int16)), (i, r)

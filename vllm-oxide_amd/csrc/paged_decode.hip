@@ -1472,24 +1472,24 @@ CascadeLayout cascade_layout(int64_t batch, int64_t num_heads, int64_t num_kv_he
   return c;
 }
 
-// The side stream of overlapped cascaded calls on each device, with the two
-// events that fork it from and join it back into the caller's stream (both are
-// capturable: under HIP graph capture the fork and the join become graph edges).
-// Created on a device's first overlapped call and kept for the process, at the
-// default priority.  Callers hold g_side_mutex from the fork to the join's
-// enqueue, so calls from several host threads each wait for their own work.
+// The side stream of overlapped cascaded calls, one per host thread and device,
+// with the two events that fork it from and join it back into the caller's stream
+// (both capturable: under HIP graph capture the fork and the join become graph
+// edges).  Created on the thread's first overlapped call on a device and kept
+// until the process ends, at the default priority.  Per thread, so calls from
+// several host threads (or graphs captured in several threads) never share one:
+// each fork and join brackets that call's own work.
 struct SideStream {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
   bool tried = false, ok = false;
 };
 constexpr int kMaxSideDevices = 64;
-std::mutex g_side_mutex;
-SideStream g_side[kMaxSideDevices];
-SideStream* side_stream_locked() {
+thread_local SideStream t_side[kMaxSideDevices];
+SideStream* side_stream() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxSideDevices) return nullptr;
-  SideStream& t = g_side[dev];
+  SideStream& t = t_side[dev];
   if (!t.tried) {
     t.tried = true;
     oxide::RelaxedCaptureScope relaxed;
@@ -1531,7 +1531,9 @@ extern "C" int paged_decode_attention_shared_prefix_plan(int64_t batch, int64_t 
       page_block_size <= 0 || shared_blocks_hint <= 0 || num_heads % num_kv_heads != 0)
     return kCascadePlain;
   const int64_t group = num_heads / num_kv_heads;
-  if (!stream_ok(batch, num_kv_heads) || !(group <= 8 || group == 16)) return kCascadePlain;
+  if (!stream_ok(batch, num_kv_heads) || !(group <= 8 || group == 16) || (head_dim != 64 && head_dim != 128) ||
+      page_block_size % 16 != 0)
+    return kCascadePlain;
   const int64_t hint = std::min(shared_blocks_hint, ceil_div(max_seqlen_k, page_block_size));
   if (!cascade_pays(batch, num_kv_heads, head_dim, page_block_size, hint)) return kCascadePlain;
   const CascadeLayout c = cascade_layout(batch, num_heads, num_kv_heads, head_dim, page_block_size, max_seqlen_k, hint);
@@ -1681,8 +1683,7 @@ void decode_attention_impl(bool compact_ws, int forced_path, void* out, const vo
     if (cl.reserve > 0) {
       // The prefix pass on the side stream, the stream pass on the caller's stream
       // over the other CUs; the merge waits for both.
-      std::lock_guard<std::mutex> lock(g_side_mutex);
-      SideStream* side = side_stream_locked();
+      SideStream* side = side_stream();
       if (side != nullptr) {
         int wgs = device_cu_count();
         wgs -= wgs % kXcds;
