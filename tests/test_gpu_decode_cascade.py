@@ -140,6 +140,42 @@ def test_cascade_vs_oracle(device, case, append, mode):
         assert np.array_equal(caches[0], want_caches[0]) and np.array_equal(caches[1], want_caches[1])
 
 
+def _random_cases(n, seed):
+    """Seeded random shapes: kv heads 1 / 2 / 4 / 8, groups 1 / 2 / 4 / 8 / 16, D 64 / 128,
+    pages 16 / 32 / 64 / 256, ragged lengths (some shorter than the shared prefix, some
+    empty), a window on half of them, an oversized hint on some, a diverging row on some."""
+    rng = np.random.default_rng(seed)
+    out = []
+    while len(out) < n:
+        Hkv = int(rng.choice([1, 2, 4, 8]))
+        G = int(rng.choice([1, 2, 4, 8, 16]))
+        D = int(rng.choice([64, 128]))
+        BS = int(rng.choice([16, 32, 64, 256]))
+        B = int(rng.integers(2, 40))
+        shared = int(rng.integers(1, max(2, 2048 // BS)))
+        extra = [int(x) for x in rng.integers(-shared * BS // 2, 900, size=B)]
+        if B > 3:
+            extra[int(rng.integers(0, B))] = -shared * BS  # an empty sequence
+        window = int(rng.integers(10, 2500)) if rng.random() < 0.5 else -1
+        hint = shared + int(rng.integers(0, 3))
+        diverge = {int(rng.integers(1, B)): int(rng.integers(0, shared))} if rng.random() < 0.3 else None
+        dtype = "bf16" if rng.random() < 0.7 else "f16"
+        out.append((B, G * Hkv, Hkv, D, BS, shared, extra, window, hint, dtype, diverge))
+    return out
+
+
+RANDOM_CASES = _random_cases(12, 2024)
+
+
+@pytest.mark.parametrize("case", RANDOM_CASES, ids=[f"r{i}" for i in range(len(RANDOM_CASES))])
+@pytest.mark.parametrize("mode", ["serial", "overlap"])
+def test_cascade_random_shapes(device, case, mode):
+    print(f"cascade random case {case[:7]} window={case[7]} hint={case[8]} {case[9]} {mode}", flush=True)
+    got, want, _, _ = _run(device, case, False, mode)
+    assert_attn_close(got, want)
+    assert_attn_scaled(got, want, label=f"cascade random {case[:5]}")
+
+
 def test_cascade_plan_by_shape(device):
     """The by-shape form: the plain entries where the cascade saves under 200 MB of K/V
     reads (small batches), the cascade beyond, overlapped when the per-sequence part is long
