@@ -489,6 +489,86 @@ static void test_gpu_decode_step() {
   for (void* p : {dk, dv, dq, dout, ds}) (void)hipFree(p);
 }
 
+// DecodeStep over a batch whose block tables share their first 16 blocks (one
+// cached 4096-token prompt, block_pool.rs:133-142 sharing; each sequence's own
+// blocks after it): upload counts the shared blocks, run_layer takes the cascaded
+// entry (the plan runs the cascade at this size), and the output matches the plain
+// entry's on the same cache within the attention tolerance.
+static void test_gpu_decode_step_shared_prefix() {
+  const std::size_t Hq = 32, H = 8, D = 128, BS = 256, B = 64, S = 16;
+  std::vector<uint32_t> lens(B);
+  std::vector<std::vector<int32_t>> tables(B);
+  int32_t next = static_cast<int32_t>(S);
+  for (std::size_t b = 0; b < B; ++b) {
+    lens[b] = static_cast<uint32_t>(S * BS + 1 + (b * 37) % 900);
+    for (std::size_t j = 0; j < S; ++j) tables[b].push_back(static_cast<int32_t>(j));
+    for (std::size_t j = S * BS; j < lens[b]; j += BS) tables[b].push_back(next++);
+  }
+  const std::size_t NB = static_cast<std::size_t>(next);
+  PagedKVCache cache(1, NB, BS, H, D, OXIDE_DTYPE_BF16);
+  DecodeStep step(cache, Hq);
+  uint64_t s = 99;
+  auto rnd = [&s]() {
+    s = s * 6364136223846793005ULL + 1442695040888963407ULL;
+    return static_cast<float>(static_cast<int64_t>(s >> 11) % 2000 - 1000) / 1000.f;
+  };
+  const std::size_t cache_elems = NB * BS * H * D;
+  std::vector<uint16_t> host(cache_elems);
+  for (void* dst : {cache.k_cache(0), cache.v_cache(0)}) {
+    for (auto& x : host) x = f2bf(rnd());
+    (void)hipMemcpy(dst, host.data(), host.size() * 2, hipMemcpyHostToDevice);
+  }
+  std::vector<uint16_t> q(B * Hq * D), kn(B * H * D), vn(B * H * D);
+  for (auto& x : q) x = f2bf(rnd());
+  for (auto& x : kn) x = f2bf(rnd());
+  for (auto& x : vn) x = f2bf(rnd());
+  std::vector<int64_t> slots(B);
+  for (std::size_t b = 0; b < B; ++b)
+    slots[b] = static_cast<int64_t>(tables[b][(lens[b] - 1) / BS]) * BS + (lens[b] - 1) % BS;
+  void *dq, *dk, *dv, *do1, *do2;
+  (void)hipMalloc(&dq, q.size() * 2);
+  (void)hipMalloc(&dk, kn.size() * 2);
+  (void)hipMalloc(&dv, vn.size() * 2);
+  (void)hipMalloc(&do1, q.size() * 2);
+  (void)hipMalloc(&do2, q.size() * 2);
+  (void)hipMemcpy(dq, q.data(), q.size() * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(dk, kn.data(), kn.size() * 2, hipMemcpyHostToDevice);
+  (void)hipMemcpy(dv, vn.data(), vn.size() * 2, hipMemcpyHostToDevice);
+  const AttnMetadata meta = build_decode_metadata(lens, tables, slots);
+  step.upload(meta, nullptr);
+  CHECK(step.shared_blocks() == S);
+  const float scale = 1.f / std::sqrt(static_cast<float>(D));
+  CHECK(paged_decode_attention_shared_prefix_plan(B, Hq, H, D, BS, meta.max_seqlen_k, S) != 3);
+  step.run_layer(0, dq, dk, dv, do1, scale, -1, nullptr);
+  CHECK(hipDeviceSynchronize() == hipSuccess);
+  // The plain entry on the same cache (the new tokens are in place now).
+  const PaddedTable t = pad_block_table(tables);
+  void *dcu, *dtab, *dws;
+  const std::size_t ws = paged_decode_attention_workspace_size(B, Hq, H, D, meta.max_seqlen_k);
+  (void)hipMalloc(&dcu, meta.cu_seqlens_k.size() * 4);
+  (void)hipMalloc(&dtab, t.data.size() * 4);
+  (void)hipMalloc(&dws, ws);
+  (void)hipMemcpy(dcu, meta.cu_seqlens_k.data(), meta.cu_seqlens_k.size() * 4, hipMemcpyHostToDevice);
+  (void)hipMemcpy(dtab, t.data.data(), t.data.size() * 4, hipMemcpyHostToDevice);
+  paged_decode_attention(do2, dq, cache.k_cache(0), cache.v_cache(0), static_cast<const uint32_t*>(dcu),
+                         static_cast<const int32_t*>(dtab), static_cast<int64_t>(t.width), static_cast<int64_t>(NB),
+                         B, Hq, H, D, BS, meta.max_seqlen_k, -1, scale, dws, ws, OXIDE_DTYPE_BF16, nullptr);
+  CHECK(oxide_last_error() == OXIDE_OK);
+  CHECK(hipDeviceSynchronize() == hipSuccess);
+  std::vector<uint16_t> o1(q.size()), o2(q.size());
+  (void)hipMemcpy(o1.data(), do1, o1.size() * 2, hipMemcpyDeviceToHost);
+  (void)hipMemcpy(o2.data(), do2, o2.size() * 2, hipMemcpyDeviceToHost);
+  double max_err = 0;
+  for (std::size_t i = 0; i < o1.size(); ++i) {
+    CHECK(!std::isnan(bf2f(o1[i])));
+    max_err = std::max(max_err, static_cast<double>(std::fabs(bf2f(o1[i]) - bf2f(o2[i]))));
+  }
+  CHECK(max_err <= 2e-2);
+  std::printf("decode step, shared prefix: %zu shared blocks, max |cascade - plain| %.3g\n", step.shared_blocks(),
+              max_err);
+  for (void* p : {dq, dk, dv, do1, do2, dcu, dtab, dws}) (void)hipFree(p);
+}
+
 // PrefillStep: a 24-token prompt behind a 40-token cached prefix (two sequences'
 // worth of checks in one: the prefix keys come from the cache, the prompt's from
 // the append).  Positions 0 and no q/k norm make the prologue an exact split of
@@ -650,6 +730,7 @@ int main(int argc, char** argv) {
     test_gpu_cow_all_layers();
     test_gpu_prefill_step();
     test_gpu_decode_step();
+    test_gpu_decode_step_shared_prefix();
   } else {
     std::printf("usage: test_host cpu|gpu|div [full]|hash <seed> <hex>\n");
     return 2;

@@ -2,7 +2,8 @@
 
 CPU: block pool, slot mapping, metadata, padding and layout, restating the
 reference's unit tests; XXH64 of the host layer against python-xxhash.
-GPU: PagedKVCache append known answer and a DecodeStep against fp64 softmax."""
+GPU: PagedKVCache append known answer, a DecodeStep against fp64 softmax, and a
+DecodeStep over a shared-prefix batch (the cascaded entry) against the plain entry."""
 import subprocess
 from pathlib import Path
 

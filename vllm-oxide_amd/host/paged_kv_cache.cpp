@@ -149,10 +149,30 @@ void DecodeStep::upload(const AttnMetadata& meta, hipStream_t stream) {
                        hipMemcpyHostToDevice, stream), "upload block_table");
   check(hipMemcpyAsync(d_slots_, h_slots_.data(), h_slots_.size() * sizeof(int64_t),
                        hipMemcpyHostToDevice, stream), "upload slot_mapping");
-  const std::size_t ws = paged_decode_attention_workspace_size(
-      static_cast<int64_t>(batch_), static_cast<int64_t>(num_heads_),
-      static_cast<int64_t>(cache_.num_kv_heads()), static_cast<int64_t>(cache_.head_dim()),
-      static_cast<int64_t>(max_seqlen_k_));
+  // Leading entries every row holds (bounded by the shortest row).
+  shared_blocks_ = 0;
+  if (batch_ > 1) {
+    std::size_t n = meta.block_table[0].size();
+    for (const auto& row : meta.block_table) n = std::min(n, row.size());
+    while (shared_blocks_ < n) {
+      const int32_t id = meta.block_table[0][shared_blocks_];
+      bool same = true;
+      for (const auto& row : meta.block_table) same = same && row[shared_blocks_] == id;
+      if (!same) break;
+      ++shared_blocks_;
+    }
+  }
+  const std::size_t ws =
+      shared_blocks_ > 0
+          ? paged_decode_attention_shared_prefix_workspace_size(
+                static_cast<int64_t>(batch_), static_cast<int64_t>(num_heads_),
+                static_cast<int64_t>(cache_.num_kv_heads()), static_cast<int64_t>(cache_.head_dim()),
+                static_cast<int64_t>(cache_.block_size()), static_cast<int64_t>(max_seqlen_k_),
+                static_cast<int64_t>(shared_blocks_))
+          : paged_decode_attention_workspace_size(
+                static_cast<int64_t>(batch_), static_cast<int64_t>(num_heads_),
+                static_cast<int64_t>(cache_.num_kv_heads()), static_cast<int64_t>(cache_.head_dim()),
+                static_cast<int64_t>(max_seqlen_k_));
   ensure(&d_ws_, &cap_ws_, std::max<std::size_t>(ws, 1));
 }
 
@@ -161,7 +181,20 @@ void DecodeStep::run_layer(std::size_t layer, const void* q, const void* key, co
                            hipStream_t stream) {
   if (batch_ == 0) return;
   // Append then attend, fused into one launch (same result as reshape_and_cache
-  // followed by paged_decode_attention).
+  // followed by paged_decode_attention); with a shared prefix the cascaded entry,
+  // which runs the plain one where the cascade would not pay.
+  if (shared_blocks_ > 0) {
+    ::paged_decode_attention_shared_prefix(
+        out, q, key, value, static_cast<const int64_t*>(d_slots_), cache_.k_cache(layer),
+        cache_.v_cache(layer), static_cast<const uint32_t*>(d_cu_), static_cast<const int32_t*>(d_table_),
+        static_cast<int64_t>(max_blocks_), static_cast<int64_t>(cache_.num_blocks()),
+        static_cast<int64_t>(batch_), static_cast<int64_t>(num_heads_),
+        static_cast<int64_t>(cache_.num_kv_heads()), static_cast<int64_t>(cache_.head_dim()),
+        static_cast<int64_t>(cache_.block_size()), static_cast<int64_t>(max_seqlen_k_), window_left,
+        softmax_scale, static_cast<int64_t>(shared_blocks_), d_ws_, cap_ws_, cache_.dtype(), stream);
+    check_lib("paged_decode_attention_shared_prefix");
+    return;
+  }
   ::paged_decode_attention_append(
       out, q, key, value, static_cast<const int64_t*>(d_slots_), cache_.k_cache(layer),
       cache_.v_cache(layer), static_cast<const uint32_t*>(d_cu_),

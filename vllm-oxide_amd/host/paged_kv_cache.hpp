@@ -71,22 +71,30 @@ class DecodeStep {
 
   // Uploads cu_seqlens_k, the 0-padded block table and the slot mapping of
   // this step (asynchronous on `stream`; the host copy stays alive inside).
+  // Also counts the leading block-table entries every row holds in common: the
+  // prefix blocks the BlockPool handed to every sequence (block_pool.rs:133-142
+  // sharing), the hint of the cascaded attention entry.
   void upload(const AttnMetadata& meta, hipStream_t stream);
 
   // Layer `layer`: append key/value [B, Hkv, D], then decode attention of
   // q [B, Hq, D] into out [B, Hq, D] (the order of models/qwen3.rs:199-208),
-  // as one fused launch (paged_decode_attention_append).
+  // as one fused launch (paged_decode_attention_append; with a shared prefix,
+  // paged_decode_attention_shared_prefix, which attends the shared blocks once
+  // for the batch where that pays).
   void run_layer(std::size_t layer, const void* q, const void* key, const void* value, void* out,
                  float softmax_scale, int32_t window_left, hipStream_t stream);
 
   std::size_t batch() const { return batch_; }
+  // Leading block-table entries common to every row of the uploaded step (0 for
+  // a batch of one).
+  std::size_t shared_blocks() const { return shared_blocks_; }
 
  private:
   void ensure(void** ptr, std::size_t* cap, std::size_t bytes);
 
   const PagedKVCache& cache_;
   std::size_t num_heads_;
-  std::size_t batch_ = 0, max_blocks_ = 0, max_seqlen_k_ = 0;
+  std::size_t batch_ = 0, max_blocks_ = 0, max_seqlen_k_ = 0, shared_blocks_ = 0;
   std::vector<uint32_t> h_cu_;
   std::vector<int32_t> h_table_;
   std::vector<int64_t> h_slots_;
