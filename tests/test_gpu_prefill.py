@@ -77,6 +77,11 @@ CASES = [
     ([100, 33], [100, 66], 4, 2, 64, 16, 7, "bf16"),                  # G=2, D=64, window 7
     ([90], [300], 32, 2, 64, 256, -1, "f16"),                         # G=16, D=64
     ([40], [40], 24, 8, 128, 256, -1, "bf16"),                        # G=3 (rows not a power of 2)
+    # No cached prefix and prompts of at most 2048 tokens: workgroups take row tiles in
+    # pairs (n - 1 - i, then i), including an odd tile count's middle tile alone.
+    ([70, 33], [70, 33], 32, 8, 128, 256, -1, "bf16"),                # 3 and 2 row tiles
+    ([300, 150], [300, 150], 32, 8, 128, 64, 50, "f16"),              # window 50, BS=64
+    ([2048], [2048], 16, 8, 64, 32, -1, "bf16"),                      # the longest paired prompt
 ]
 
 

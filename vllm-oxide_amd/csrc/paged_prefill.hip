@@ -37,7 +37,8 @@
 // Workgroup order is XCD-aware: all row tiles of one (sequence, kv head) run
 // on one XCD (workgroup i runs on XCD i % 8), so its K/V is fetched from HBM
 // once into that XCD's L2 and re-read from there; within a unit the tiles
-// with the most keys (last tokens) start first.
+// with the most keys (last tokens) start first.  For short prompts (kPair) a
+// workgroup takes two row tiles of its unit, n - 1 - i and then i.
 #include <math.h>
 
 #include <algorithm>
@@ -92,6 +93,7 @@ struct PrefillParams {
   int shared_hint;
   int dec_batch;
   int* shared_out;  // the number of shared blocks found (written by workgroup 0)
+  int pair;         // 1: each workgroup takes row tiles n - 1 - i and then i of its unit
 };
 
 __device__ __forceinline__ int clamp_len(int64_t n, int cap) {
@@ -147,7 +149,7 @@ enum PrefillAddressing {
   kPagedRows = 2,   // paged, any block_size: a block lookup per row
 };
 
-template <class Tag, int D, int MODE, bool kPrefix>
+template <class Tag, int D, int MODE, bool kPrefix, bool kPair = false>
 __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParams p) {
   constexpr int CH = D / 8;                  // 16-byte chunks per head row
   constexpr int KS = D / 16;                 // MFMA k-steps of Q.K (16 dims each)
@@ -170,9 +172,16 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
   // unit (key split, kv head), all of them over table row 0 (the shared entries).
   const int i = blockIdx.x;
   const int j = i / kPfXcds;
-  const int u = (j / p.tiles_per_unit) * kPfXcds + i % kPfXcds;
+  const int wpu = kPair ? (p.tiles_per_unit + 1) / 2 : p.tiles_per_unit;  // workgroups per unit
+  const int u = (j / wpu) * kPfXcds + i % kPfXcds;
   if (u >= p.units) return;
-  const int tile = p.tiles_per_unit - 1 - j % p.tiles_per_unit;
+  const int jj = j % wpu;
+  for (int pass = 0; pass < (kPair ? 2 : 1); ++pass) {
+  const int tile = pass == 0 ? p.tiles_per_unit - 1 - jj : jj;
+  if (pass == 1) {
+    if (tile >= p.tiles_per_unit - 1 - jj) break;  // the middle tile of an odd count: done
+    __syncthreads();  // the previous tile's last LDS reads before this tile's first loads
+  }
   const int b = kPrefix ? 0 : u / p.num_kv_heads;
   const int kh = u % p.num_kv_heads;
   const int split = kPrefix ? u / p.num_kv_heads : 0;
@@ -184,13 +193,13 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
     if (blockIdx.x == 0 && threadIdx.x == 0) *p.shared_out = shared;
     Lq = p.dec_batch;
     Lk = shared * p.block_size;  // the shared keys; no sequence attends past them here
-    if (split * p.split_keys >= Lk) return;
+    if (split * p.split_keys >= Lk) continue;
   } else {
     Lq = clamp_len(static_cast<int64_t>(p.cu_seqlens_q[b + 1]) - p.cu_seqlens_q[b], p.max_seqlen_q);
     Lk = clamp_len(static_cast<int64_t>(p.cu_seqlens_k[b + 1]) - p.cu_seqlens_k[b], p.max_seqlen_k);
   }
   const int t0 = tile * p.tokens_per_wg;
-  if (t0 >= Lq) return;
+  if (t0 >= Lq) continue;
   const int t1 = min(Lq, t0 + p.tokens_per_wg);
   const int off = Lk - Lq;  // hi of token t is t + off
   const int G = p.group;
@@ -494,12 +503,22 @@ __global__ __launch_bounds__(kPfThreads, 2) void paged_prefill_attn(PrefillParam
         *reinterpret_cast<uint2*>(op + 32 * db + 8 * q) = w;
       }
   }
+  }
 }
 
 int64_t ceil_div64(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 template <class Tag, int D>
 void launch_mode(const PrefillParams& p, dim3 grid, hipStream_t s) {
+  if (p.pair) {
+    if (p.block_table == nullptr)
+      hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kContiguous, false, true>), grid, dim3(kPfThreads), 0, s, p);
+    else if (p.block_size % kPfKeys == 0)
+      hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedTiles, false, true>), grid, dim3(kPfThreads), 0, s, p);
+    else
+      hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kPagedRows, false, true>), grid, dim3(kPfThreads), 0, s, p);
+    return;
+  }
   if (p.block_table == nullptr)
     hipLaunchKernelGGL((paged_prefill_attn<Tag, D, kContiguous, false>), grid, dim3(kPfThreads), 0, s, p);
   else if (p.block_size % kPfKeys == 0)
@@ -519,7 +538,7 @@ void launch_prefix_mode(const PrefillParams& p, dim3 grid, hipStream_t s) {
 template <class Tag>
 bool launch_prefill(const PrefillParams& p, int head_dim, hipStream_t s) {
   const int64_t units8 = ceil_div64(p.units, kPfXcds) * kPfXcds;
-  const dim3 grid(static_cast<unsigned>(units8 * p.tiles_per_unit));
+  const dim3 grid(static_cast<unsigned>(units8 * (p.pair ? (p.tiles_per_unit + 1) / 2 : p.tiles_per_unit)));
   if (head_dim == 128) {
     launch_mode<Tag, 128>(p, grid, s);
     return true;
@@ -598,6 +617,13 @@ void prefill_impl(void* out, const void* q, const void* k, const void* v, const 
   }
   p.tiles_per_unit = static_cast<int>(tiles);
   p.units = static_cast<int>(units);
+  // Short prompts with no cached prefix: a workgroup takes a unit's row tiles n - 1 - i
+  // and then i (a separate kernel instance), the same keys per workgroup and half the
+  // workgroup starts.  Measured on MI355X, Qwen3-8B heads, bit-identical output:
+  // 16 x 1024 212.1 -> 202.8 us, 32 x 512 138.6 -> 135.7 us, 8 x 2048 324.2 -> 319.9 us;
+  // for 4 x 4096 and 1 x 8192 pairing measured +0.7 / +1.3 %, and with a cached prefix
+  // the tiles already carry equal keys.
+  p.pair = (tiles >= 2 && max_seqlen_k <= max_seqlen_q && max_seqlen_q <= 2048) ? 1 : 0;
   p.block_size = static_cast<int>(block_table ? page_block_size : 1);
   p.window_left = window_left < 0 ? -1 : window_left;
   p.scale_log2 = softmax_scale * 1.4426950408889634f;
