@@ -733,9 +733,13 @@ def decode_main(args) -> int:
         # here; `--prefill` / `--prologue` run them alone with theirs): paged prefill
         # attention at two prompt shapes (matrix-core roofline) and the fused q/k norm +
         # RoPE + KV append over 16k tokens (HBM roofline).
+        # ~60 ms of warm-up calls each: the first calls of a run of these MFMA-bound kernels
+        # run slower while the clocks ramp (measured, 20 timed calls: 4 x 4096 673 us after
+        # 5 warm-up calls, 598 us after 50, 581 us after 100 with 200 timed; 16 x 1024 254 /
+        # 227 / 205 us).
         extra["prefill"] = {m["workload"]: m for m in
-                            (measure_prefill(dev, 4, 4096, 0, args.seed, 20, 5),
-                             measure_prefill(dev, 16, 1024, 0, args.seed, 20, 5))}
+                            (measure_prefill(dev, 4, 4096, 0, args.seed, 40, 100),
+                             measure_prefill(dev, 16, 1024, 0, args.seed, 100, 300))}
         # 300 warm-up calls: the first ~200 calls of a run of these short kernels are ~12 %
         # slower (measured: 82 us for calls 20-220, then 72 us).
         extra["prologue"] = measure_prologue(dev, 16384, args.seed, 200, 300)
