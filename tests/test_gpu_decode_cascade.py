@@ -356,3 +356,54 @@ def test_cascade_overlapped_from_two_threads(device):
     for i in range(2):
         for r in range(5):
             assert torch.equal(outs[i][r].view(torch.int16), want[i].view(torch.int16)), (i, r)
+
+
+_CASCADE_CAPTURE_FIRST = r'''
+import math, sys
+sys.path[:0] = [{repo!r}, {pkg!r}, {tests!r}]
+import numpy as np
+import torch
+import oxide_paged_kv as ox
+import test_gpu_decode_cascade as T
+from helpers import to_torch
+
+dev = torch.device("cuda:0")
+B, Hq, Hkv, D, BS, shared, extra, window, hint, dtype, diverge = T.CASES[12]
+q, kc, vc, cu, table, mx, lens = T._shared_case(41, B, Hq, Hkv, D, BS, shared, extra, dtype, diverge)
+t = lambda a: to_torch(a, dtype, dev)
+qd, kd, vd = t(q), t(kc), t(vc)
+cu_d = torch.from_numpy(cu.view(np.int32)).to(dev)
+bt_d = torch.from_numpy(table).to(dev)
+ws = torch.zeros(ox.shared_prefix_workspace_size(B, Hq, Hkv, D, BS, mx, hint), dtype=torch.uint8, device=dev)
+out = torch.empty_like(qd)
+kw = dict(shared_prefix_blocks=hint, shared_prefix_mode="overlap")
+ox.load()
+torch.cuda.synchronize()
+# The library's first call in this process -- the one that creates the side stream -- is captured.
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, 1 / math.sqrt(D), None, BS, out=out, workspace=ws, **kw)
+for rep in range(2):
+    out.fill_(0)
+    graph.replay()
+    torch.cuda.synchronize()
+    want = ox.decode_attn(qd, kd, vd, cu_d, bt_d, mx, 1 / math.sqrt(D), None, BS, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16)), rep
+print("cascade capture-first ok", flush=True)
+'''
+
+
+def test_cascade_first_call_under_graph_capture():
+    """In a fresh process whose first library call is an overlapped cascaded call under HIP
+    graph capture (the side stream and its events are created during the capture), the
+    replays equal the eager call bit for bit."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    repo = Path(__file__).resolve().parent.parent
+    code = _CASCADE_CAPTURE_FIRST.format(repo=str(repo), pkg=str(repo / "vllm-oxide_amd"), tests=str(repo / "tests"))
+    print("cascade capture-first subprocess", flush=True)
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=110)
+    assert r.returncode == 0 and "cascade capture-first ok" in r.stdout, r.stdout[-2000:] + r.stderr[-4000:]

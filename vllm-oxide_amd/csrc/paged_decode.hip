@@ -1482,7 +1482,7 @@ CascadeLayout cascade_layout(int64_t batch, int64_t num_heads, int64_t num_kv_he
 struct SideStream {
   hipStream_t stream = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
-  bool tried = false, ok = false;
+  bool ok = false;
 };
 constexpr int kMaxSideDevices = 64;
 thread_local SideStream t_side[kMaxSideDevices];
@@ -1490,16 +1490,19 @@ SideStream* side_stream() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxSideDevices) return nullptr;
   SideStream& t = t_side[dev];
-  if (!t.tried) {
-    t.tried = true;
+  if (!t.ok) {
+    // (Re)tried on each call until it succeeds: a call that cannot create them (say,
+    // under a capture mode that forbids it) runs its passes one after the other.
     oxide::RelaxedCaptureScope relaxed;
     // The events order work on this device only (the prefix pass's partials are read by
     // the merge on the same device), so they skip the system-scope fence, which makes
     // memory visible to the host and to other devices (cfg4: 108.7 -> 105.6 us).
     constexpr unsigned kFlags = hipEventDisableTiming | hipEventDisableSystemFence;
-    t.ok = hipStreamCreateWithFlags(&t.stream, hipStreamNonBlocking) == hipSuccess &&
-           hipEventCreateWithFlags(&t.fork, kFlags) == hipSuccess &&
-           hipEventCreateWithFlags(&t.join, kFlags) == hipSuccess;
+    if (!t.stream && hipStreamCreateWithFlags(&t.stream, hipStreamNonBlocking) != hipSuccess) t.stream = nullptr;
+    if (!t.fork && hipEventCreateWithFlags(&t.fork, kFlags) != hipSuccess) t.fork = nullptr;
+    if (!t.join && hipEventCreateWithFlags(&t.join, kFlags) != hipSuccess) t.join = nullptr;
+    t.ok = t.stream && t.fork && t.join;
+    if (!t.ok) (void)hipGetLastError();  // a failed creation leaves no error for the launch check
   }
   return t.ok ? &t : nullptr;
 }
