@@ -396,7 +396,7 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=None, help="timed steps (default 200; --prologue 500)")
-    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 100; --prologue 50)")
+    ap.add_argument("--warmup", type=int, default=None, help="untimed steps (default 100; --prologue 300)")
     ap.add_argument("--config", type=int, default=3)
     ap.add_argument("--layers", type=int, default=0, help="distinct layers to rotate over (0 = auto)")
     ap.add_argument("--seed", type=int, default=0)
@@ -420,7 +420,8 @@ def main() -> int:
     if args.steps is None:
         args.steps = 500 if args.prologue else 200
     if args.warmup is None:
-        args.warmup = 50 if args.prologue else 100
+        # The prologue's first ~200 calls run slower while the clocks ramp.
+        args.warmup = 300 if args.prologue else 100
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
