@@ -88,6 +88,32 @@ def test_workspace_and_split_policy():
     assert ox.workspace_size(64, 32, 8, 128, 0) == 0
 
 
+def test_cascade_plan_and_workspace():
+    """The cascaded entry's host policy (no launch): the plain entries where sharing
+    saves under 200 MB of K/V reads, the cascade beyond, overlapped when the per-sequence
+    part is long enough to hide the shared-key pass; shapes the stream pass does not take
+    and a zero hint run the plain entries; the workspace covers both forms and the plain
+    one.  Without a GPU the CU count reads as 256."""
+    import oxide_paged_kv as ox
+
+    plan = ox.shared_prefix_plan
+    assert plan(4, 32, 8, 128, 256, 8192 + 256, 32) == "plain"        # 100 MB saved
+    assert plan(64, 32, 8, 128, 256, 1024 + 3000, 4) == "overlap"     # 264 MB, long private parts
+    assert plan(128, 32, 8, 128, 256, 4096 + 100, 16) == "serial"     # short private parts
+    assert plan(128, 32, 8, 128, 256, 5120, 16) == "overlap"          # cfg4
+    assert plan(128, 32, 8, 128, 256, 5120, 0) == "plain"
+    assert plan(128, 36, 6, 128, 256, 5120, 16) == "plain"            # kv heads not dividing 8
+    assert plan(128, 32, 8, 96, 256, 5120, 16) == "plain"             # head_dim not built
+    ws = ox.shared_prefix_workspace_size(128, 32, 8, 128, 256, 5120, 16)
+    assert ws >= ox.workspace_size(128, 32, 8, 128, 5120)
+    # prefix partials: at least one split row per (sequence, head) plus the whole-sequence rows
+    assert ws >= 2 * 128 * 32 * (128 + 1) * 4
+    # a larger hint never needs less workspace; the hint is clamped to the longest sequence
+    assert ox.shared_prefix_workspace_size(128, 32, 8, 128, 256, 5120, 8) <= ws
+    assert ox.shared_prefix_workspace_size(128, 32, 8, 128, 256, 5120, 10 ** 6) == \
+        ox.shared_prefix_workspace_size(128, 32, 8, 128, 256, 5120, 20)
+
+
 def test_no_cpu_fallback_when_library_missing(tmp_path, monkeypatch):
     from oxide_paged_kv import _lib
 
